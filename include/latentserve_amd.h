@@ -1,0 +1,118 @@
+/*
+ * latentserve_amd — C ABI of the MI355X (gfx950) paged GQA decode-attention
+ * library (liblatentserve_hip.so).
+ *
+ * Plain pointers, sizes and element strides; no framework types.  Every
+ * device pointer is a HIP device allocation; `stream` is a hipStream_t (NULL
+ * = the default stream).  Calls only enqueue work on `stream`: no host
+ * synchronisation, no device-to-host reads, no allocation — every buffer,
+ * including scratch, is the caller's, so the calls can be captured in a
+ * HIP graph.  Return value: 0 on success, else an LS_ERR_* code with a
+ * message from ls_last_error() (thread-local).
+ *
+ * Layouts (strides in elements, innermost dimension unit-stride):
+ *   q           [B, H_kv, n_rep, 128] fp16        strides q_strides[3] = (b, h, r)
+ *   k/v pool    [num_blocks, 16, H_kv, 128]       strides kv_strides[3] = (block, token, head)
+ *   block_tables[B, max_pages] int32              row stride bt_stride
+ *   seq_lens    [B] int32
+ *   k_scale     [num_blocks, H_kv, 128] fp32      ks_strides[2] = (block, head)
+ *   v_scale     [num_blocks, 16, H_kv]  fp32      vs_strides[3] = (block, token, head)
+ *   k_zero/v_zero: as k_scale / v_scale (asymmetric INT8 only, else NULL)
+ *   k_residual  [R, 16, H_kv, 128] fp16           res_strides[3] = (row, token, head)
+ *   res_rows    [B] int32 (row of k_residual holding each sequence's last page)
+ *   out         [B, H_kv, n_rep, 128] fp16        out_strides[3] = (b, h, r)
+ *   part_acc    fp32 [B, H_kv, num_splits, n_rep, 128]  contiguous scratch
+ *   part_m/l    fp32 [B, H_kv, num_splits, n_rep]       contiguous scratch
+ *   counters    int32 [B * H_kv], zero before the first call; every call
+ *               leaves it zero again.  Calls that share scratch must be
+ *               ordered on one stream.
+ *
+ * The reference (Jash-Vora/LatentServe) has no C ABI: its kernels are CuPy
+ * launches of extern "C" __global__ functions with positional pointer and
+ * stride arguments.  Each entry point below names the reference interface it
+ * replaces.
+ */
+#ifndef LATENTSERVE_AMD_H
+#define LATENTSERVE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    LS_OK = 0,
+    LS_ERR_INVALID = 1,    /* shape, dtype-size, alignment or pointer check failed */
+    LS_ERR_HIP = 2,        /* the HIP runtime rejected the launch */
+};
+
+/* Message for the last non-zero return on this thread. */
+const char* ls_last_error(void);
+
+/* ABI version (bumped on any signature change). */
+int ls_abi_version(void);
+
+/* fp16 paged decode.  Replaces paged_decode_fp16 + the Triton combine, i.e.
+ * paged_decode_cuda() for an fp16 pool (kernels/cuda/paged_decode_cuda.py:202-252,
+ * kernels/cuda/paged_decode_fp16.cu:55-64) behind paged_decode_attention
+ * (kernels/gqa/paged_decode.py:709-829).  Pages per split are derived on the
+ * device from seq_lens (paged_decode_fp16.cu:79-83).  With num_splits == 1
+ * the output is written directly and the part_* and counters buffers are not
+ * touched (they may be NULL). */
+int ls_paged_decode_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
+                         const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                         const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                         const int32_t* seq_lens, void* out, const int64_t* out_strides,
+                         float* part_acc, float* part_m, float* part_l, int32_t* counters,
+                         int batch, int kv_heads, int n_rep, int head_dim, int page,
+                         int num_splits, float softmax_scale, void* stream);
+
+/* INT8 paged decode.  Replaces paged_decode_int8 (kernels/cuda/paged_decode_int8.cu:87-102;
+ * launcher kernels/cuda/paged_decode_cuda.py:236-244).  k_scale/v_scale
+ * required (fp32); k_zero and v_zero both or neither; k_residual with
+ * res_rows (res_capacity = rows in k_residual) or neither. */
+int ls_paged_decode_int8(const void* q, const int64_t* q_strides, const void* k_pool,
+                         const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                         const float* k_scale, const int64_t* ks_strides, const float* v_scale,
+                         const int64_t* vs_strides, const float* k_zero, const float* v_zero,
+                         const void* k_residual, const int64_t* res_strides, int res_capacity,
+                         const int32_t* res_rows, const int32_t* block_tables, int64_t bt_stride,
+                         int max_pages, const int32_t* seq_lens, void* out,
+                         const int64_t* out_strides, float* part_acc, float* part_m,
+                         float* part_l, int32_t* counters, int batch, int kv_heads, int n_rep,
+                         int head_dim, int page, int num_splits, float softmax_scale,
+                         void* stream);
+
+/* Page-subset (sparse) decode over sel[b, h, 0:n] logical pages, fp16 pool.
+ * Replaces paged_sparse_fp16 (kernels/cuda/paged_sparse_fp16.cu:205-217; launcher
+ * sparse_decode, kernels/cuda/paged_sparse.py:185-219).  With ratio > 0 each
+ * sequence attends its first max(recent+1, ceilf(ratio*pages)) entries, capped
+ * at its pages and num_sel; ratio <= 0 attends all num_sel.  Entries outside
+ * [0, pages) are skipped. */
+int ls_paged_sparse_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
+                         const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                         const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                         const int32_t* seq_lens, const int32_t* sel, const int64_t* sel_strides,
+                         int num_sel, float ratio, int recent, void* out,
+                         const int64_t* out_strides, float* part_acc, float* part_m,
+                         float* part_l, int32_t* counters, int batch, int kv_heads, int n_rep,
+                         int head_dim, int page, int num_splits, float softmax_scale,
+                         void* stream);
+
+/* Merge split partials: combine_splits / _combine_kernel
+ * (kernels/gqa/paged_decode.py:689-706, :422-471).  acc [B, H, S, rows, 128]
+ * with strides acc_strides[4] = (b, h, s, row); m and l [B, H, S, rows] with
+ * ml_strides[3] = (b, h, s), unit row stride, m in natural-log units; out
+ * [B, H, n_rep, 128] fp16 (out_fp32 = 0) or fp32 (out_fp32 = 1). */
+int ls_combine_splits(const float* part_acc, const int64_t* acc_strides, const float* part_m,
+                      const float* part_l, const int64_t* ml_strides, void* out, int out_fp32,
+                      const int64_t* out_strides, int batch, int kv_heads, int num_splits,
+                      int n_rep, int head_dim, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LATENTSERVE_AMD_H */

@@ -1,0 +1,96 @@
+"""ctypes binding of liblatentserve_hip.so (the C ABI in include/latentserve_amd.h).
+
+The library is built in-tree by ``python -m latentserve_amd.csrc.build``.
+There is no fallback: if it is missing or fails to load, every entry point
+raises, so a GPU run can never silently take another path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblatentserve_hip.so")
+
+_VP = ctypes.c_void_p
+_I64P = ctypes.POINTER(ctypes.c_int64)
+_I32 = ctypes.c_int
+_F32 = ctypes.c_float
+_I64 = ctypes.c_int64
+
+LS_ERR_INVALID = 1
+LS_ERR_HIP = 2
+
+# name -> argtypes, mirroring include/latentserve_amd.h
+_SIGNATURES = {
+    "ls_abi_version": [],
+    "ls_last_error": [],
+    "ls_paged_decode_fp16": [
+        _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
+        _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
+    "ls_paged_decode_int8": [
+        _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64P, _VP, _I64P, _VP, _VP,
+        _VP, _I64P, _I32, _VP, _VP, _I64, _I32, _VP, _VP, _I64P,
+        _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
+    "ls_paged_sparse_fp16": [
+        _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
+        _I32, _F32, _I32, _VP, _I64P, _VP, _VP, _VP, _VP,
+        _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
+    "ls_combine_splits": [
+        _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class HipLibraryMissing(RuntimeError):
+    pass
+
+
+def exported_symbols() -> list[str]:
+    return sorted(_SIGNATURES)
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library (once). Raises HipLibraryMissing if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HipLibraryMissing(
+                f"{LIB_PATH} is not built; run `python -m latentserve_amd.csrc.build` "
+                "(the HIP backend has no fallback)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_char_p if name == "ls_last_error" else ctypes.c_int
+        _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == 0:
+        return
+    msg = lib().ls_last_error().decode(errors="replace")
+    if rc == LS_ERR_INVALID:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def ptr(t: Optional[torch.Tensor]):
+    return None if t is None else _VP(t.data_ptr())
+
+
+def strides(t: Optional[torch.Tensor], n: int):
+    if t is None:
+        return None
+    return (ctypes.c_int64 * n)(*t.stride()[:n])
+
+
+def stream_of(device: torch.device):
+    """torch's current stream on `device` as a hipStream_t."""
+    return _VP(torch.cuda.current_stream(device).cuda_stream)

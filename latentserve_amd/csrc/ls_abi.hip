@@ -1,0 +1,268 @@
+// C ABI of liblatentserve_hip.so: argument checks, then one launch on the
+// caller's stream.  Declared in include/latentserve_amd.h.
+//
+// The checks are what the reference's eligible() / paged_decode_cuda() raise
+// on (kernels/cuda/paged_decode_cuda.py:105-141, 214-217), plus what a
+// gfx950 launch must not violate: 16-byte vector loads need 16-byte aligned
+// rows, the lane mapping needs head_dim 128 and 16-token pages, and the grid's
+// y dimension is the batch.
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/latentserve_amd.h"
+#include "ls_common.h"
+#include "ls_decode.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(LS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return LS_OK;
+}
+
+bool aligned(const void* p, size_t n) { return ((uintptr_t)p % n) == 0; }
+
+// Base pointer and every listed stride (in elements of `elem` bytes) must be
+// `n`-byte aligned for the kernels' vector loads.
+bool rows_aligned(const void* p, const int64_t* st, int count, size_t elem, size_t n) {
+    if (!aligned(p, n)) return false;
+    for (int i = 0; i < count; ++i)
+        if ((st[i] * (int64_t)elem) % (int64_t)n != 0) return false;
+    return true;
+}
+
+int check_common(const void* q, const int64_t* q_strides, const void* k_pool, const void* v_pool,
+                 const int64_t* kv_strides, int num_blocks, const int32_t* block_tables,
+                 int max_pages, const int32_t* seq_lens, void* out, const int64_t* out_strides,
+                 float* part_acc, float* part_m, float* part_l, int32_t* counters, int batch,
+                 int kv_heads, int n_rep, int head_dim, int page, int num_splits, size_t kv_elem) {
+    if (!q || !q_strides || !k_pool || !v_pool || !kv_strides || !block_tables || !seq_lens ||
+        !out || !out_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim != ls::HEAD_DIM) return fail(LS_ERR_INVALID, "head_dim must be 128, got %d", head_dim);
+    if (page != ls::PAGE) return fail(LS_ERR_INVALID, "page (block_size) must be 16, got %d", page);
+    if (n_rep < 1 || n_rep > ls::MAX_NREP)
+        return fail(LS_ERR_INVALID, "n_rep must be in [1, 16], got %d", n_rep);
+    if (batch < 0 || batch > 65535) return fail(LS_ERR_INVALID, "batch must be in [0, 65535], got %d", batch);
+    if (kv_heads < 1) return fail(LS_ERR_INVALID, "kv_heads must be >= 1, got %d", kv_heads);
+    if (num_splits < 1 || (int64_t)num_splits * kv_heads > (1LL << 31) - 1)
+        return fail(LS_ERR_INVALID, "num_splits must be >= 1, got %d", num_splits);
+    if (num_blocks < 1) return fail(LS_ERR_INVALID, "num_blocks must be >= 1");
+    if (max_pages < 1) return fail(LS_ERR_INVALID, "max_pages (block-table width) must be >= 1");
+    if (!rows_aligned(q, q_strides, 3, 2, 16))
+        return fail(LS_ERR_INVALID, "q rows must be 16-byte aligned");
+    if (!rows_aligned(k_pool, kv_strides, 3, kv_elem, kv_elem == 2 ? 16 : 8) ||
+        !rows_aligned(v_pool, kv_strides, 3, kv_elem, kv_elem == 2 ? 16 : 8))
+        return fail(LS_ERR_INVALID, "K/V pool rows must be %d-byte aligned", kv_elem == 2 ? 16 : 8);
+    if (!aligned(out, 2)) return fail(LS_ERR_INVALID, "out must be 2-byte aligned");
+    if (num_splits > 1 && (!part_acc || !part_m || !part_l || !counters))
+        return fail(LS_ERR_INVALID, "num_splits > 1 needs part_acc, part_m, part_l and counters");
+    (void)out_strides;
+    return LS_OK;
+}
+
+void fill_common(ls::DecodeParams& a, const void* q, const int64_t* q_strides, const void* k_pool,
+                 const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                 const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                 const int32_t* seq_lens, void* out, const int64_t* out_strides, float* part_acc,
+                 float* part_m, float* part_l, int32_t* counters, int batch, int kv_heads,
+                 int n_rep, int num_splits, float softmax_scale) {
+    memset(&a, 0, sizeof a);
+    a.q = (const _Float16*)q;
+    a.sq_b = q_strides[0];
+    a.sq_h = q_strides[1];
+    a.sq_r = q_strides[2];
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.sk_b = kv_strides[0];
+    a.sk_p = kv_strides[1];
+    a.sk_h = kv_strides[2];
+    a.block_tables = block_tables;
+    a.sbt_b = bt_stride;
+    a.max_pages = max_pages;
+    a.num_blocks = num_blocks;
+    a.seq_lens = seq_lens;
+    a.part_acc = part_acc;
+    a.part_m = part_m;
+    a.part_l = part_l;
+    a.counters = counters;
+    a.out = (_Float16*)out;
+    a.so_b = out_strides[0];
+    a.so_h = out_strides[1];
+    a.so_r = out_strides[2];
+    a.B = batch;
+    a.H = kv_heads;
+    a.NR = n_rep;
+    a.num_splits = num_splits;
+    a.scale = softmax_scale;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ls_last_error(void) { return g_err.c_str(); }
+
+int ls_abi_version(void) { return 1; }
+
+int ls_paged_decode_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
+                         const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                         const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                         const int32_t* seq_lens, void* out, const int64_t* out_strides,
+                         float* part_acc, float* part_m, float* part_l, int32_t* counters,
+                         int batch, int kv_heads, int n_rep, int head_dim, int page,
+                         int num_splits, float softmax_scale, void* stream) {
+    int rc = check_common(q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables,
+                          max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l,
+                          counters, batch, kv_heads, n_rep, head_dim, page, num_splits, 2);
+    if (rc) return rc;
+    if (batch == 0) return LS_OK;
+    ls::DecodeParams a;
+    fill_common(a, q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables, bt_stride,
+                max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l, counters, batch,
+                kv_heads, n_rep, num_splits, softmax_scale);
+    a.kind = ls::KV_FP16;
+    return hip_status(ls::launch_decode(a, (hipStream_t)stream), "ls_paged_decode_fp16");
+}
+
+int ls_paged_decode_int8(const void* q, const int64_t* q_strides, const void* k_pool,
+                         const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                         const float* k_scale, const int64_t* ks_strides, const float* v_scale,
+                         const int64_t* vs_strides, const float* k_zero, const float* v_zero,
+                         const void* k_residual, const int64_t* res_strides, int res_capacity,
+                         const int32_t* res_rows, const int32_t* block_tables, int64_t bt_stride,
+                         int max_pages, const int32_t* seq_lens, void* out,
+                         const int64_t* out_strides, float* part_acc, float* part_m,
+                         float* part_l, int32_t* counters, int batch, int kv_heads, int n_rep,
+                         int head_dim, int page, int num_splits, float softmax_scale,
+                         void* stream) {
+    int rc = check_common(q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables,
+                          max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l,
+                          counters, batch, kv_heads, n_rep, head_dim, page, num_splits, 1);
+    if (rc) return rc;
+    if (!k_scale || !ks_strides || !v_scale || !vs_strides)
+        return fail(LS_ERR_INVALID, "INT8 pools need k_scale and v_scale");
+    if (!rows_aligned(k_scale, ks_strides, 2, 4, 16))
+        return fail(LS_ERR_INVALID, "k_scale rows must be 16-byte aligned");
+    if (!aligned(v_scale, 4)) return fail(LS_ERR_INVALID, "v_scale must be 4-byte aligned");
+    if ((k_zero == nullptr) != (v_zero == nullptr))
+        return fail(LS_ERR_INVALID, "k_zero and v_zero go together");
+    if (k_zero && !aligned(k_zero, 16))
+        return fail(LS_ERR_INVALID, "k_zero must be 16-byte aligned");
+    if (v_zero && !aligned(v_zero, 4)) return fail(LS_ERR_INVALID, "v_zero must be 4-byte aligned");
+    if ((k_residual == nullptr) != (res_rows == nullptr))
+        return fail(LS_ERR_INVALID, "k_residual and res_rows go together");
+    if (k_residual) {
+        if (!res_strides) return fail(LS_ERR_INVALID, "k_residual needs res_strides");
+        if (!rows_aligned(k_residual, res_strides, 3, 2, 16))
+            return fail(LS_ERR_INVALID, "k_residual rows must be 16-byte aligned");
+        if (res_capacity < 1) return fail(LS_ERR_INVALID, "res_capacity must be >= 1");
+    }
+    if (batch == 0) return LS_OK;
+    ls::DecodeParams a;
+    fill_common(a, q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables, bt_stride,
+                max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l, counters, batch,
+                kv_heads, n_rep, num_splits, softmax_scale);
+    a.kind = ls::KV_INT8;
+    a.k_scale = k_scale;
+    a.sks_b = ks_strides[0];
+    a.sks_h = ks_strides[1];
+    a.v_scale = v_scale;
+    a.svs_b = vs_strides[0];
+    a.svs_p = vs_strides[1];
+    a.svs_h = vs_strides[2];
+    a.k_zero = k_zero;
+    a.v_zero = v_zero;
+    a.k_res = (const _Float16*)k_residual;
+    if (k_residual) {
+        a.sr_r = res_strides[0];
+        a.sr_p = res_strides[1];
+        a.sr_h = res_strides[2];
+        a.res_cap = res_capacity;
+        a.res_rows = res_rows;
+    }
+    return hip_status(ls::launch_decode(a, (hipStream_t)stream), "ls_paged_decode_int8");
+}
+
+int ls_paged_sparse_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
+                         const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                         const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                         const int32_t* seq_lens, const int32_t* sel, const int64_t* sel_strides,
+                         int num_sel, float ratio, int recent, void* out,
+                         const int64_t* out_strides, float* part_acc, float* part_m,
+                         float* part_l, int32_t* counters, int batch, int kv_heads, int n_rep,
+                         int head_dim, int page, int num_splits, float softmax_scale,
+                         void* stream) {
+    int rc = check_common(q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables,
+                          max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l,
+                          counters, batch, kv_heads, n_rep, head_dim, page, num_splits, 2);
+    if (rc) return rc;
+    if (!sel || !sel_strides) return fail(LS_ERR_INVALID, "sparse decode needs sel");
+    if (num_sel < 0) return fail(LS_ERR_INVALID, "num_sel must be >= 0");
+    if (batch == 0) return LS_OK;
+    ls::DecodeParams a;
+    fill_common(a, q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables, bt_stride,
+                max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l, counters, batch,
+                kv_heads, n_rep, num_splits, softmax_scale);
+    a.kind = ls::KV_FP16;
+    a.sel = sel;
+    a.ssel_b = sel_strides[0];
+    a.ssel_h = sel_strides[1];
+    a.num_sel = num_sel;
+    a.ratio = ratio;
+    a.recent = recent;
+    return hip_status(ls::launch_decode(a, (hipStream_t)stream), "ls_paged_sparse_fp16");
+}
+
+int ls_combine_splits(const float* part_acc, const int64_t* acc_strides, const float* part_m,
+                      const float* part_l, const int64_t* ml_strides, void* out, int out_fp32,
+                      const int64_t* out_strides, int batch, int kv_heads, int num_splits,
+                      int n_rep, int head_dim, void* stream) {
+    if (!part_acc || !acc_strides || !part_m || !part_l || !ml_strides || !out || !out_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim != ls::HEAD_DIM) return fail(LS_ERR_INVALID, "head_dim must be 128, got %d", head_dim);
+    if (n_rep < 1 || num_splits < 1 || kv_heads < 1 || batch < 0)
+        return fail(LS_ERR_INVALID, "bad combine shape");
+    if ((int64_t)batch * kv_heads > (1LL << 31) - 1) return fail(LS_ERR_INVALID, "grid too large");
+    if (batch == 0) return LS_OK;
+    ls::CombineParams p;
+    p.acc = part_acc;
+    p.sa_b = acc_strides[0];
+    p.sa_h = acc_strides[1];
+    p.sa_s = acc_strides[2];
+    p.sa_r = acc_strides[3];
+    p.m = part_m;
+    p.l = part_l;
+    p.sm_b = ml_strides[0];
+    p.sm_h = ml_strides[1];
+    p.sm_s = ml_strides[2];
+    p.out = out;
+    p.out_f32 = out_fp32 ? 1 : 0;
+    p.so_b = out_strides[0];
+    p.so_h = out_strides[1];
+    p.so_r = out_strides[2];
+    p.B = batch;
+    p.H = kv_heads;
+    p.S = num_splits;
+    p.NR = n_rep;
+    return hip_status(ls::launch_combine(p, (hipStream_t)stream), "ls_combine_splits");
+}
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+// Shared device helpers for the gfx950 paged-decode kernels.
+//
+// Wave64 throughout.  Every kernel here is written for CDNA4 directly: 64-lane
+// wavefronts, 16x16x16 f16 MFMA tiles, cross-lane traffic by ds_bpermute /
+// readlane, no warp-32 assumptions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ls {
+
+typedef _Float16 half_t;
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+constexpr int HEAD_DIM = 128;   // the lane mapping below covers exactly 128 channels
+constexpr int PAGE = 16;        // one page = the M=16 side of a 16x16 MFMA tile
+constexpr int MAX_NREP = 16;    // query rows per KV head = the N=16 side of the tile
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+
+// 2^x on the transcendental unit (v_exp_f32): exact 0 for -inf.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+    const int lane = __lane_id();
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2,
+                                                                   __builtin_bit_cast(int, v)));
+}
+
+// Max / sum over the four 16-lane groups that share a lane's `lane & 15`.
+__device__ __forceinline__ float group4_max(float v) {
+    v = fmaxf(v, shfl_xor(v, 16));
+    return fmaxf(v, shfl_xor(v, 32));
+}
+__device__ __forceinline__ float group4_sum(float v) {
+    v += shfl_xor(v, 16);
+    return v + shfl_xor(v, 32);
+}
+
+// Four signed int8 (one dword) -> four fp16, exactly: each byte, offset by
+// 128, is spliced under the exponent of 1024.0h (0x64xx = 1024 + xx) and the
+// 1152 bias is removed with one packed fp16 subtract per pair.
+__device__ __forceinline__ u2 i8x4_to_h4(uint32_t x) {
+    const uint32_t u = x ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2 bias = {(half_t)1152.0f, (half_t)1152.0f};
+    const h2 a = __builtin_bit_cast(h2, lo) - bias;
+    const h2 b = __builtin_bit_cast(h2, hi) - bias;
+    u2 r;
+    r.x = __builtin_bit_cast(uint32_t, a);
+    r.y = __builtin_bit_cast(uint32_t, b);
+    return r;
+}
+
+__device__ __forceinline__ h4 as_h4(uint32_t lo, uint32_t hi) {
+    u2 t;
+    t.x = lo;
+    t.y = hi;
+    return __builtin_bit_cast(h4, t);
+}
+
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+    return __builtin_nontemporal_load(p);
+}
+
+}  // namespace ls

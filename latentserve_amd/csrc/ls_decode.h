@@ -1,0 +1,64 @@
+// Internal launch descriptors shared by the kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ls {
+
+enum KvKind { KV_FP16 = 0, KV_INT8 = 1 };
+
+// Everything one decode launch reads.  Strides are in elements.
+struct DecodeParams {
+    const _Float16* q;
+    int64_t sq_b, sq_h, sq_r;
+    const void* k_pool;
+    const void* v_pool;
+    int64_t sk_b, sk_p, sk_h;          // shared by K and V
+    int kind;
+    const float* k_scale;
+    int64_t sks_b, sks_h;
+    const float* v_scale;
+    int64_t svs_b, svs_p, svs_h;
+    const float* k_zero;               // same strides as k_scale
+    const float* v_zero;               // same strides as v_scale
+    const _Float16* k_res;
+    int64_t sr_r, sr_p, sr_h;
+    const int32_t* res_rows;
+    const int32_t* block_tables;
+    int64_t sbt_b;
+    int max_pages;                     // block-table width: pages past it are not read
+    int num_blocks;                    // pool size: out-of-range block ids are not read
+    int res_cap;                       // residual rows: out-of-range res_rows are not read
+    const int32_t* seq_lens;
+    const int32_t* sel;                // page-subset walk when non-null
+    int64_t ssel_b, ssel_h;
+    int num_sel;
+    float ratio;
+    int recent;
+    float* part_acc;                   // [B, H, S, NR, 128] contiguous
+    float* part_m;                     // [B, H, S, NR] contiguous, natural-log units
+    float* part_l;                     // [B, H, S, NR] contiguous
+    int32_t* counters;                 // [B * H], zero at rest, reset by the kernel
+    _Float16* out;
+    int64_t so_b, so_h, so_r;
+    int B, H, NR, num_splits;
+    float scale;
+};
+
+struct CombineParams {
+    const float* acc;
+    int64_t sa_b, sa_h, sa_s, sa_r;
+    const float* m;
+    const float* l;
+    int64_t sm_b, sm_h, sm_s;          // shared by m and l, unit stride over rows
+    void* out;
+    int out_f32;
+    int64_t so_b, so_h, so_r;
+    int B, H, S, NR;
+};
+
+hipError_t launch_decode(const DecodeParams& a, hipStream_t stream);
+hipError_t launch_combine(const CombineParams& p, hipStream_t stream);
+
+}  // namespace ls

@@ -1,0 +1,212 @@
+"""The MI355X paged decode backend: HIP kernels behind a C ABI.
+
+Mirrors the reference's CUDA backend module (kernels/cuda/paged_decode_cuda.py):
+``eligible`` (:112-141), ``choose_splits`` (:197-199) and the launcher
+``paged_decode_cuda`` (:202-252), here ``paged_decode_hip``. The same
+arguments, the same ValueErrors for non-unit strides / non-int32 tables, the
+same return value (a ``[B, H_kv, n_rep, D]`` view of a persistent fp16 buffer).
+
+What differs is underneath: one launch per call (the split combine is fused
+into the decode kernel: the last workgroup of each (sequence, head) merges
+the partials), MFMA tiles instead of scalar FMAs, and no runtime compilation —
+the library is built ahead of time for gfx950.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from latentserve_amd import _lib
+from latentserve_amd.kernels.gqa import _scratch as scratch
+
+HEAD_DIM = 128
+PAGE = 16
+MAX_NREP = 16
+# Waves per workgroup in the decode kernel (each walks every NW-th page of
+# its split); must match NWAVES in csrc/ls_decode.hip.
+WAVES_PER_GROUP = 4
+MAX_SPLITS = 1024
+
+_CU_COUNT: dict = {}
+
+
+def _cus(device: torch.device) -> int:
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    if dev not in _CU_COUNT:
+        _CU_COUNT[dev] = torch.cuda.get_device_properties(dev).multi_processor_count
+    return _CU_COUNT[dev]
+
+
+def choose_splits(batch: int, kv_heads: int, num_pages: int,
+                  device: Optional[torch.device] = None) -> int:
+    """Splits per (sequence, KV head) for the MI355X kernel.
+
+    Enough workgroups for about three resident groups per CU (each group is
+    four waves streaming pages), but never so many that a wave gets fewer
+    than two pages. Fixed by (batch, heads, pages) alone, so a captured graph
+    can pin it per context bucket.
+    """
+    cus = _cus(device) if device is not None and torch.cuda.is_available() else 256
+    target_groups = 3 * cus
+    by_cus = -(-target_groups // max(1, batch * kv_heads))
+    by_pages = max(1, num_pages // (2 * WAVES_PER_GROUP))
+    return max(1, min(MAX_SPLITS, by_cus, by_pages))
+
+
+def ineligible_reason(q: torch.Tensor, k_pool: torch.Tensor, k_scale=None, k_residual=None,
+                      v_scale=None, k_zero=None, v_zero=None, res_rows=None) -> Optional[str]:
+    """Why the HIP kernels cannot take these inputs, or None.
+
+    The reference's rules (kernels/cuda/paged_decode_cuda.py:112-141) plus the
+    tile shape: head_dim 128, 16-token pages, at most 16 query rows per KV head.
+    """
+    if not q.is_cuda or not k_pool.is_cuda:
+        return "tensors are not on a GPU"
+    if q.dtype != torch.float16:
+        return f"q must be float16, got {q.dtype}"
+    if q.dim() != 4 or q.shape[-1] != HEAD_DIM:
+        return f"q must be [B, H_kv, n_rep, {HEAD_DIM}]"
+    if not 1 <= q.shape[2] <= MAX_NREP:
+        return f"n_rep must be in [1, {MAX_NREP}], got {q.shape[2]}"
+    if k_pool.dim() != 4 or k_pool.shape[1] != PAGE or k_pool.shape[-1] != HEAD_DIM:
+        return f"pools must be [num_blocks, {PAGE}, H_kv, {HEAD_DIM}]"
+    if k_pool.shape[2] != q.shape[1]:
+        return "q and the pools disagree on H_kv"
+    if not _aligned(q, 16):
+        return "q rows must be 16-byte aligned and unit-stride"
+    if k_pool.dtype == torch.float16:
+        if k_scale is not None or k_residual is not None:
+            return "an fp16 pool takes no scales or residual"
+        return None if _aligned(k_pool, 16) else "pool rows must be 16-byte aligned"
+    if k_pool.dtype != torch.int8:
+        return f"pools must be float16 or int8, got {k_pool.dtype}"
+    if k_scale is None or v_scale is None:
+        return "an INT8 pool needs k_scale and v_scale"
+    if not _aligned(k_pool, 8):
+        return "INT8 pool rows must be 8-byte aligned"
+    if k_scale.dtype != torch.float32 or v_scale.dtype != torch.float32:
+        return "scales must be float32"
+    if not _aligned(k_scale, 16):
+        return "k_scale rows must be 16-byte aligned"
+    if (k_zero is None) != (v_zero is None):
+        return "k_zero and v_zero go together"
+    if k_zero is not None and (k_zero.dtype != torch.float32 or k_zero.stride() != k_scale.stride()
+                               or v_zero.stride() != v_scale.stride() or not _aligned(k_zero, 16)):
+        return "zero points must be float32 with their scales' strides"
+    if (k_residual is None) != (res_rows is None):
+        return "k_residual and res_rows go together"
+    if k_residual is not None and (k_residual.dtype != torch.float16 or not _aligned(k_residual, 16)
+                                   or res_rows.dtype != torch.int32):
+        return "k_residual must be aligned float16 and res_rows int32"
+    return None
+
+
+def eligible(q: torch.Tensor, k_pool: torch.Tensor, k_scale=None, k_residual=None,
+             v_scale=None, k_zero=None, v_zero=None, res_rows=None) -> bool:
+    """kernels/cuda/paged_decode_cuda.py:112-141, for the HIP kernels."""
+    return ineligible_reason(q, k_pool, k_scale, k_residual, v_scale, k_zero, v_zero,
+                             res_rows) is None
+
+
+def _aligned(t: torch.Tensor, nbytes: int) -> bool:
+    return (t.stride(-1) == 1 and t.data_ptr() % nbytes == 0
+            and all((st * t.element_size()) % nbytes == 0 for st in t.stride()[:-1]))
+
+
+def _buffers(tag: str, b: int, h: int, splits: int, n_rep: int, device):
+    """Persistent output and split scratch for one shape (graph-address stable)."""
+    out = scratch(f"{tag}_out", (b, h, MAX_NREP, HEAD_DIM), torch.float16, device)
+    if splits == 1:
+        return out, None, None, None, None
+    acc = scratch(f"{tag}_acc", (b, h, splits, n_rep, HEAD_DIM), torch.float32, device)
+    m = scratch(f"{tag}_m", (b, h, splits, n_rep), torch.float32, device)
+    l = scratch(f"{tag}_l", (b, h, splits, n_rep), torch.float32, device)
+    # Arrival counters: zero at rest, and every launch leaves them zero.
+    cnt = scratch(f"{tag}_cnt", (b * h,), torch.int32, device, init=0)
+    return out, acc, m, l, cnt
+
+
+def _check_common(q, k_pool, v_pool, block_tables, seq_lens):
+    if q.stride(-1) != 1 or k_pool.stride(-1) != 1 or v_pool.stride() != k_pool.stride():
+        raise ValueError("the HIP kernel needs unit-stride head dims and matching K/V pools")
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise ValueError("block tables and sequence lengths must be int32")
+    if block_tables.stride(-1) != 1 or seq_lens.stride(-1) != 1:
+        raise ValueError("block tables and sequence lengths must be unit-stride")
+    if v_pool.dtype != k_pool.dtype or v_pool.shape != k_pool.shape:
+        raise ValueError("K and V pools must match in dtype and shape")
+    for t in (k_pool, v_pool, block_tables, seq_lens):
+        if t.device != q.device:
+            raise ValueError("all tensors must be on q's device")
+
+
+def paged_decode_hip(q, k_pool, v_pool, block_tables, seq_lens, max_seq_len: int,
+                     num_splits: Optional[int] = None,
+                     softmax_scale: Optional[float] = None,
+                     k_scale=None, v_scale=None, k_zero=None, v_zero=None,
+                     k_residual=None, res_rows=None) -> torch.Tensor:
+    """Paged decode on the HIP kernels -> [B, H_kv, n_rep, D] (q.dtype).
+
+    kernels/cuda/paged_decode_cuda.py:202-252. The returned tensor is a view
+    of a persistent buffer, overwritten by the next call of the same shape.
+    """
+    reason = ineligible_reason(q, k_pool, k_scale, k_residual, v_scale, k_zero, v_zero, res_rows)
+    if reason is not None:
+        raise ValueError(f"paged_decode_hip: {reason}")
+    _check_common(q, k_pool, v_pool, block_tables, seq_lens)
+    b, h_kv, n_rep, d = q.shape
+    num_pages = -(-int(max_seq_len) // PAGE)
+    splits = int(num_splits) if num_splits else choose_splits(b, h_kv, num_pages, q.device)
+    splits = max(1, min(MAX_SPLITS, splits))
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
+    is_int8 = k_pool.dtype == torch.int8
+    out, acc, m, l, cnt = _buffers("hip_i8" if is_int8 else "hip", b, h_kv, splits, n_rep,
+                                   q.device)
+    L = _lib.lib()
+    P, S = _lib.ptr, _lib.strides
+    common_tail = (P(out), S(out, 3), P(acc), P(m), P(l), P(cnt), b, h_kv, n_rep, d,
+                   k_pool.shape[1], splits, float(scale), _lib.stream_of(q.device))
+    if is_int8:
+        rc = L.ls_paged_decode_int8(
+            P(q), S(q, 3), P(k_pool), P(v_pool), S(k_pool, 3), k_pool.shape[0],
+            P(k_scale), S(k_scale, 2), P(v_scale), S(v_scale, 3), P(k_zero), P(v_zero),
+            P(k_residual), S(k_residual, 3), 0 if k_residual is None else k_residual.shape[0],
+            P(res_rows), P(block_tables), block_tables.stride(0), block_tables.shape[1],
+            P(seq_lens), *common_tail)
+        _lib.check(rc, "ls_paged_decode_int8")
+    else:
+        rc = L.ls_paged_decode_fp16(
+            P(q), S(q, 3), P(k_pool), P(v_pool), S(k_pool, 3), k_pool.shape[0],
+            P(block_tables), block_tables.stride(0), block_tables.shape[1], P(seq_lens),
+            *common_tail)
+        _lib.check(rc, "ls_paged_decode_fp16")
+    return out[:, :, :n_rep]
+
+
+def combine_splits_hip(partial_acc: torch.Tensor, partial_m: torch.Tensor,
+                       partial_l: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    """combine_splits (kernels/gqa/paged_decode.py:689-706) as one HIP launch.
+
+    partial_acc [B, H, S, N_REP, D] fp32, partial_m/l [B, H, S, N_REP] fp32
+    (natural-log maxima) -> [B, H, N_REP, D] in out_dtype (fp16 or fp32).
+    """
+    if out_dtype not in (torch.float16, torch.float32):
+        raise ValueError("out_dtype must be float16 or float32")
+    for t in (partial_acc, partial_m, partial_l):
+        if t.dtype != torch.float32 or not t.is_cuda:
+            raise ValueError("partials must be float32 GPU tensors")
+    if partial_m.stride() != partial_l.stride() or partial_m.stride(-1) != 1 \
+            or partial_acc.stride(-1) != 1:
+        raise ValueError("m and l must share strides; rows and channels unit-stride")
+    b, h, s, nr, d = partial_acc.shape
+    out = torch.empty((b, h, nr, d), dtype=out_dtype, device=partial_acc.device)
+    rc = _lib.lib().ls_combine_splits(
+        _lib.ptr(partial_acc), _lib.strides(partial_acc, 4), _lib.ptr(partial_m),
+        _lib.ptr(partial_l), _lib.strides(partial_m, 3), _lib.ptr(out),
+        1 if out_dtype == torch.float32 else 0, _lib.strides(out, 3), b, h, s, nr, d,
+        _lib.stream_of(partial_acc.device))
+    _lib.check(rc, "ls_combine_splits")
+    return out
