@@ -1,0 +1,298 @@
+"""Paged GQA decode attention on one MI355X: µs per layer-step and HBM GB/s.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--splits S]
+
+A "step" is one layer-step: one paged-decode call (one kernel launch) over
+one layer's KV pool for the whole batch. The workload rotates through 28
+distinct layer pools (Qwen2.5-1.5B depth) so that neither L2 nor the 256 MB
+MALL can serve a layer's 268 MB from cache; 28 calls are captured in one HIP
+graph and the graph is replayed, timed with HIP events on the launch stream.
+
+Configs: c1 B1x2048, c2 B16x16384 (the headline), c3
+B8x32768, c3r ragged B16 with lengths ~U[512, 32768], c4 INT8 B16x16384.
+Inputs are synthetic N(0,1) fp16 from a seeded device generator; block
+tables are a seeded permutation of the pool (non-contiguous pages).
+
+Prints ONE JSON line. `value` is the achieved algorithmic HBM bandwidth
+(bytes the path must read and write per layer-step / measured time).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+LAYERS = 28
+H_KV, N_REP, D, PAGE = 2, 6, 128, 16
+
+CONFIGS = {
+    "c1": dict(batch=1, ctx=2048, kind="fp16", workload="fp16 paged decode B1 x 2048"),
+    "c2": dict(batch=16, ctx=16384, kind="fp16", workload="fp16 paged decode B16 x 16384"),
+    "c3": dict(batch=8, ctx=32768, kind="fp16", workload="fp16 paged decode B8 x 32768"),
+    "c3r": dict(batch=16, ctx=32768, kind="fp16", ragged=True,
+                workload="fp16 paged decode B16 ragged L~U[512,32768]"),
+    "c4": dict(batch=16, ctx=16384, kind="int8",
+               workload="INT8 paged decode B16 x 16384 (fp32 scales, fp16 last-page K residual)"),
+}
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2800)
+    p.add_argument("--warmup", type=int, default=280)
+    p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    p.add_argument("--splits", type=int, default=None)
+    p.add_argument("--layers", type=int, default=LAYERS)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seqs", type=int, default=None,
+                   help="sequences in the CPU-baseline sample (default: the whole batch)")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                   help="instead of the benchmark, run device copies of MIB MiB (for the "
+                        "rocprof FETCH_SIZE / WRITE_SIZE scale factor) and exit")
+    return p.parse_args()
+
+
+def lengths_for(cfg, gen_seed=1234):
+    import numpy as np
+    b = cfg["batch"]
+    if cfg.get("ragged"):
+        rng = np.random.default_rng(gen_seed)
+        return rng.integers(512, cfg["ctx"] + 1, size=b).astype(np.int32)
+    return np.full(b, cfg["ctx"], np.int32)
+
+
+def algorithmic_bytes(cfg, lens) -> int:
+    """Bytes one layer-step must move: the live K/V (and INT8 scales and
+    residual), q, the live block-table entries, lengths, and the output."""
+    pages = [(int(l) + PAGE - 1) // PAGE for l in lens]
+    tokens = sum(p * PAGE for p in pages)          # whole pages are read
+    b = len(lens)
+    if cfg["kind"] == "fp16":
+        kv = tokens * H_KV * D * 2 * 2
+    else:
+        full_pages = sum(max(0, p - 1) for p in pages)
+        kv = (tokens * H_KV * D * 1 * 2                    # int8 K and V codes
+              + full_pages * H_KV * D * 4                  # K scale per (block, head, ch)
+              + tokens * H_KV * 4                          # V scale per (block, tok, head)
+              + b * PAGE * H_KV * D * 2)                   # last page of K from the residual
+    q = b * H_KV * N_REP * D * 2
+    out = q
+    tables = sum(pages) * 4 + b * 4
+    return kv + q + out + tables
+
+
+def build_workload(cfg, layers, seed=0):
+    import numpy as np
+    import torch
+
+    dev = torch.device("cuda", 0)
+    lens = lengths_for(cfg)
+    b = cfg["batch"]
+    max_pages = max(1, (int(lens.max()) + PAGE - 1) // PAGE)
+    width = (cfg["ctx"] + PAGE - 1) // PAGE
+    nb = b * width + 4
+    g = torch.Generator(device=dev).manual_seed(seed)
+    tables = torch.randperm(nb, device=dev, generator=g)[: b * width].view(b, width)
+    tables = tables.to(torch.int32).contiguous()
+    seq = torch.from_numpy(lens).to(dev)
+    pools = []
+    for _ in range(layers):
+        q = torch.randn(b, H_KV, N_REP, D, device=dev, generator=g, dtype=torch.float16)
+        k = torch.randn(nb, PAGE, H_KV, D, device=dev, generator=g, dtype=torch.float16)
+        v = torch.randn(nb, PAGE, H_KV, D, device=dev, generator=g, dtype=torch.float16)
+        if cfg["kind"] == "int8":
+            pools.append((q,) + quantize_layer(k, v, tables, seq))
+        else:
+            pools.append((q, k, v))
+    return tables, seq, pools, int(max_pages * PAGE)
+
+
+def quantize_layer(k, v, tables, seq):
+    """INT8 pools from fp16 N(0,1) data with the reference's symmetric scheme
+    (cache/int8_paged_cache.py:670-699 for K per (block, head, channel),
+    :741-758 for V per (block, token, head)); every sequence's last page of K
+    also stays in an fp16 residual, as the cache's invariant holds
+    (:283-298). Benchmark input set-up only (torch ops; not timed)."""
+    import torch
+
+    f = k.float()
+    ks = f.abs().amax(dim=1).clamp_min(1e-8) / 127
+    kq = torch.clamp(torch.round(f / ks.unsqueeze(1)), -127, 127).to(torch.int8)
+    del f
+    vf = v.float()
+    vs = vf.abs().amax(dim=-1).clamp_min(1e-8) / 127
+    vq = torch.clamp(torch.round(vf / vs.unsqueeze(-1)), -127, 127).to(torch.int8)
+    del vf
+    b = tables.shape[0]
+    last = ((seq.long() + PAGE - 1) // PAGE - 1).clamp(min=0)
+    res = k[tables[torch.arange(b, device=k.device), last].long()].contiguous()
+    res_rows = torch.arange(b, dtype=torch.int32, device=k.device)
+    return kq, vq, ks.contiguous(), vs.contiguous(), res, res_rows
+
+
+def make_call(cfg, tables, seq, layer, max_len, splits):
+    from latentserve_amd.kernels.hip import paged_decode_hip as pdh
+
+    if cfg["kind"] == "int8":
+        q, kq, vq, ks, vs, res, rr = layer
+        return lambda: pdh.paged_decode_hip(q, kq, vq, tables, seq, max_len, num_splits=splits,
+                                            k_scale=ks, v_scale=vs, k_residual=res, res_rows=rr)
+    q, k, v = layer
+    return lambda: pdh.paged_decode_hip(q, k, v, tables, seq, max_len, num_splits=splits)
+
+
+def cpu_baseline(cfg, tables, seq, layer, n_seqs):
+    """The CPU oracle (a C restatement of the reference's paged_decode_reference
+    loop) over a sample of the same workload, on this host's cores."""
+    import numpy as np
+
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    oracle.set_num_threads(threads)
+    b = cfg["batch"]
+    n = min(b, n_seqs or b)
+    lens = seq.cpu().numpy()[:n]
+    t = tables.cpu().numpy()[:n]
+    if cfg["kind"] == "int8":
+        q, kq, vq, ks, vs, res, rr = [x.cpu().numpy() for x in layer]
+        args = (q[:n], kq, vq, t, lens)
+        extra = dict(k_scale=ks, v_scale=vs, k_residual=res, res_rows=rr[:n])
+    else:
+        q, k, v = [x.cpu().numpy() for x in layer]
+        args = (q[:n], k, v, t, lens)
+        extra = {}
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.paged_decode(*args, num_splits=1, **extra)
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]                                   # median of 3
+    sample_bytes = algorithmic_bytes(cfg, lens)
+    return {
+        "value": round(sample_bytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} of {b} sequences of one layer-step ({sample_bytes / 1e6:.1f} MB), "
+                  f"C oracle (oracle/ls_oracle.c, OpenMP) with num_splits=1, median of 3: "
+                  f"{dt * 1e3:.1f} ms -> {dt * 1e3 * b / n:.1f} ms per full layer-step",
+        "ms_per_layer_step": round(dt * 1e3 * b / n, 3),
+    }
+
+
+def calibrate_copy(mib):
+    import torch
+    n = mib * (1 << 20)
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n, "launches": 5}))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU (got --gpus {args.gpus}); the decode path "
+              "shards by sequence with no exchange, so N GPUs = N x one GPU's number",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
+    cfg = CONFIGS[args.config]
+    layers = max(1, args.layers)
+    tables, seq, pools, max_len = build_workload(cfg, layers)
+    lens = seq.cpu().numpy()
+    nbytes = algorithmic_bytes(cfg, lens)
+    from latentserve_amd.kernels.hip import paged_decode_hip as pdh
+    splits = args.splits or pdh.choose_splits(cfg["batch"], H_KV, (max_len + PAGE - 1) // PAGE,
+                                              torch.device("cuda", 0))
+    calls = [make_call(cfg, tables, seq, pools[i], max_len, splits) for i in range(layers)]
+
+    for i in range(args.warmup):
+        calls[i % layers]()
+    torch.cuda.synchronize()
+
+    def capture(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                calls[i % layers]()
+        return g
+
+    full, rem = divmod(args.steps, layers)
+    g_full = capture(layers) if full else None
+    g_rem = capture(rem) if rem else None
+    if g_full is not None:
+        g_full.replay()
+    torch.cuda.synchronize()
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(full):
+        g_full.replay()
+    if g_rem is not None:
+        g_rem.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    ms_step = ms / args.steps
+    gbps = nbytes / (ms_step * 1e-3) / 1e9
+
+    result = {
+        "metric": "paged-decode attn us/layer-step + HBM GB/s (% of 8 TB/s peak), B16x16K fp16",
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "us_per_layer_step": round(ms_step * 1e3, 3),
+        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16" if cfg["kind"] == "fp16" else "int8 KV / fp16 q",
+        "data": "synthetic N(0,1), seeded device generator, permuted block tables",
+        "config": {"workload": cfg["workload"], "batch": cfg["batch"], "ctx": cfg["ctx"],
+                   "kv_heads": H_KV, "n_rep": N_REP, "head_dim": D, "page": PAGE,
+                   "layer_pools": layers, "num_splits": splits,
+                   "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_from_profiles(args.config)},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(cfg, tables, seq, pools[0], args.cpu_seqs)
+    print(json.dumps(result))
+
+
+def traffic_from_profiles(config):
+    """HBM bytes per launch from the committed rocprofv3 counter summary
+    (profiles/traffic_<config>.json: FETCH_SIZE + WRITE_SIZE per dispatch,
+    scaled by a plain copy's counter-to-bytes factor), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+if __name__ == "__main__":
+    main()

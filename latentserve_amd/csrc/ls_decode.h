@@ -44,6 +44,7 @@ struct DecodeParams {
     int64_t so_b, so_h, so_r;
     int B, H, NR, num_splits;
     float scale;
+    int fuse;                          // merge splits in the last-arriving group
 };
 
 struct CombineParams {

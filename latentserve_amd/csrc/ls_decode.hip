@@ -40,6 +40,9 @@
 //    and resets its arrival counter, so the path is one launch and safe to
 //    replay in a captured graph.
 
+#include <stdlib.h>
+#include <string.h>
+
 #include "ls_common.h"
 #include "ls_decode.h"
 
@@ -48,11 +51,24 @@ namespace ls {
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 
+// LDS scratch of combine_partials.
+constexpr int CMB_CHUNK = 64;   // splits whose weights are staged at once
+struct CombineSmem {
+    float red[16][MAX_NREP];            // per-thread-group partial max / sum
+    float mg[MAX_NREP];                 // row max over all splits
+    float lt[MAX_NREP];                 // row sum of weighted l
+    float w[CMB_CHUNK][MAX_NREP];       // weights of the current chunk of splits
+};
+
+
 template <int NW>
 struct DecodeSmem {
     float m[NW][MAX_NREP];
     float l[NW][MAX_NREP];
-    float acc[NW][MAX_NREP][HEAD_DIM];
+    union {
+        float acc[NW][MAX_NREP][HEAD_DIM];   // wave states, merged once
+        CombineSmem cmb;                     // then reused by the split combine
+    };
     int is_last;
 };
 
@@ -246,31 +262,116 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
     }
 }
 
-// Merge S partial states of one (b, h) from global memory into out (fp16),
-// the combine of kernels/gqa/paged_decode.py:689-706 / :422-471.
+// Merge S partial states of one (b, h) into out: combine_splits
+// (kernels/gqa/paged_decode.py:689-706).  256 threads.  Thread t owns row
+// r = t & 15 of split group t >> 4 for the weight passes, and float4 columns
+// of the output for the accumulation; every global load of a pass is issued
+// before any is consumed, so a pass costs one memory round trip rather than
+// one per split.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool COH>
+__device__ __forceinline__ float load_part(const float* p) {
+    if (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+}
+
+template <int VEC, bool COH = false>
 __device__ void combine_partials(const float* acc, const float* m, const float* l, int S, int NR,
                                  int64_t sa_s, int64_t sa_r, int64_t sm_s, void* out, int out_f32,
-                                 int64_t so_r, int tid, int nthreads) {
-    for (int idx = tid; idx < NR * HEAD_DIM; idx += nthreads) {
-        const int r = idx / HEAD_DIM, d = idx % HEAD_DIM;
-        float mg = neg_inf();
-        for (int s = 0; s < S; ++s) mg = fmaxf(mg, m[s * sm_s + r]);
-        float lt = 0.f, at = 0.f;
-        for (int s = 0; s < S; ++s) {
-            const float w = mg == neg_inf() ? 0.f : __expf(m[s * sm_s + r] - mg);
-            lt += l[s * sm_s + r] * w;
-            at += acc[s * sa_s + r * sa_r + d] * w;
+                                 int64_t so_r, int tid, CombineSmem& cs) {
+    const int r = tid & 15, grp = tid >> 4;
+    const bool row_ok = r < NR;
+    // pass 1: row max
+    float mx = neg_inf();
+    if (row_ok)
+        for (int s = grp; s < S; s += 16) mx = fmaxf(mx, load_part<COH>(m + s * sm_s + r));
+    cs.red[grp][r] = mx;
+    __syncthreads();
+    if (tid < MAX_NREP) {
+        float v = neg_inf();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v = fmaxf(v, cs.red[i][tid]);
+        cs.mg[tid] = v;
+    }
+    __syncthreads();
+    const float mgr = cs.mg[r];
+    const bool dead = mgr == neg_inf();
+
+    // pass 2: weights chunk by chunk, accumulating the output columns
+    constexpr int NV = HEAD_DIM / VEC;                        // vectors per row
+    constexpr int MAXO = (MAX_NREP * NV + 255) / 256;         // outputs per thread
+    const int n_out = NR * NV;
+    f4 accv[MAXO];
+#pragma unroll
+    for (int i = 0; i < MAXO; ++i) accv[i] = (f4){0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+    for (int s0 = 0; s0 < S; s0 += CMB_CHUNK) {
+        const int n = S - s0 < CMB_CHUNK ? S - s0 : CMB_CHUNK;
+        for (int i = grp; i < n; i += 16) {
+            float w = 0.f;
+            if (row_ok && !dead) {
+                w = __expf(load_part<COH>(m + (s0 + i) * sm_s + r) - mgr);
+                lsum += load_part<COH>(l + (s0 + i) * sm_s + r) * w;
+            }
+            cs.w[i][r] = w;
         }
-        const float o = at / fmaxf(lt, 1e-20f);
-        if (out_f32)
-            ((float*)out)[r * so_r + d] = o;
-        else
-            ((half_t*)out)[r * so_r + d] = (half_t)o;
+        __syncthreads();
+#pragma unroll
+        for (int oi = 0; oi < MAXO; ++oi) {
+            const int o = tid + 256 * oi;
+            if (o < n_out) {
+                const int orow = o / NV, col = (o % NV) * VEC;
+                const float* src = acc + (int64_t)s0 * sa_s + orow * sa_r + col;
+                f4 a4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 16
+                for (int i = 0; i < n; ++i) {
+                    const float w = cs.w[i][orow];
+                    if (VEC == 4) {
+                        a4 += w * *(const f4*)(src + i * sa_s);
+                    } else {
+                        a4[0] += w * load_part<COH>(src + i * sa_s);
+                    }
+                }
+                accv[oi] += a4;
+            }
+        }
+        __syncthreads();
+    }
+    // row sums of the weighted l
+    cs.red[grp][r] = lsum;
+    __syncthreads();
+    if (tid < MAX_NREP) {
+        float v = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v += cs.red[i][tid];
+        cs.lt[tid] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int oi = 0; oi < MAXO; ++oi) {
+        const int o = tid + 256 * oi;
+        if (o < n_out) {
+            const int orow = o / NV, col = (o % NV) * VEC;
+            const float inv = 1.f / fmaxf(cs.lt[orow], 1e-20f);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                const float v = accv[oi][e] * inv;
+                if (out_f32)
+                    ((float*)out)[orow * so_r + col + e] = v;
+                else
+                    ((half_t*)out)[orow * so_r + col + e] = (half_t)v;
+            }
+        }
     }
 }
 
 template <int KIND, bool ASYM, bool HAS_RES, bool SPARSE, int NW>
 __global__ __launch_bounds__(WAVE* NW) void paged_decode_kernel(const DecodeParams a) {
+    // Pages in flight ahead of the one being computed: the fp16 page buffer
+    // is 32 VGPRs, the INT8 one (codes + K scales) as large again.
+    constexpr int PF_DEPTH = KIND == KV_FP16 ? 2 : 1;
     __shared__ DecodeSmem<NW> sm;
     const int H = a.H;
     const int h = blockIdx.x % H;
@@ -375,30 +476,29 @@ __global__ __launch_bounds__(WAVE* NW) void paged_decode_kernel(const DecodePara
         }
         if (n_valid == 0) continue;
 
-        PageBuf bufA, bufB;
-        int k = 0;
-        {
-            const int p0 = __builtin_amdgcn_readlane(pg, 0);
-            const int b0 = __builtin_amdgcn_readlane(blk, 0);
-            load_page<KIND, ASYM, HAS_RES>(a, bufA, b0, p0, num_pages, b, h, g, c);
+        // Three page buffers in rotation: pages k+1 and k+2 are in flight
+        // while page k is computed.  Prefetches past the end re-read the
+        // last page (a cache hit) so every iteration waits the same way.
+        PageBuf buf[PF_DEPTH + 1];
+        const int last = n_valid - 1;
+#pragma unroll
+        for (int u = 0; u < PF_DEPTH; ++u) {
+            const int kk = u < last ? u : last;
+            load_page<KIND, ASYM, HAS_RES>(a, buf[u], __builtin_amdgcn_readlane(blk, kk),
+                                           __builtin_amdgcn_readlane(pg, kk), num_pages, b, h, g, c);
         }
-        while (true) {
-            // Prefetch the next page into the other buffer; past the end it
-            // re-reads the current page (a cache hit, keeps waits uniform).
-            const int kn = k + 1 < n_valid ? k + 1 : k;
-            const int pn = __builtin_amdgcn_readlane(pg, kn);
-            const int bn = __builtin_amdgcn_readlane(blk, kn);
-            load_page<KIND, ASYM, HAS_RES>(a, bufB, bn, pn, num_pages, b, h, g, c);
-            compute_page<KIND, ASYM>(bufA, st, qh, qf, __builtin_amdgcn_readlane(pg, k), len,
-                                     scale_log2, g);
-            if (++k >= n_valid) break;
-            const int kn2 = k + 1 < n_valid ? k + 1 : k;
-            const int pn2 = __builtin_amdgcn_readlane(pg, kn2);
-            const int bn2 = __builtin_amdgcn_readlane(blk, kn2);
-            load_page<KIND, ASYM, HAS_RES>(a, bufA, bn2, pn2, num_pages, b, h, g, c);
-            compute_page<KIND, ASYM>(bufB, st, qh, qf, __builtin_amdgcn_readlane(pg, k), len,
-                                     scale_log2, g);
-            if (++k >= n_valid) break;
+        for (int k = 0; k < n_valid;) {
+#pragma unroll
+            for (int u = 0; u <= PF_DEPTH; ++u) {
+                const int kn = k + PF_DEPTH < last ? k + PF_DEPTH : last;
+                load_page<KIND, ASYM, HAS_RES>(a, buf[(u + PF_DEPTH) % (PF_DEPTH + 1)],
+                                               __builtin_amdgcn_readlane(blk, kn),
+                                               __builtin_amdgcn_readlane(pg, kn), num_pages, b, h,
+                                               g, c);
+                compute_page<KIND, ASYM>(buf[u], st, qh, qf, __builtin_amdgcn_readlane(pg, k), len,
+                                         scale_log2, g);
+                if (++k >= n_valid) break;
+            }
         }
     }
 
@@ -440,41 +540,60 @@ __global__ __launch_bounds__(WAVE* NW) void paged_decode_kernel(const DecodePara
         if (single) {
             a.out[(int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)r * a.so_r + d] =
                 (half_t)(at / fmaxf(lt, 1e-20f));
+        } else if (a.fuse) {
+            // Device-coherent (write-through) stores: the group that merges
+            // may run on another XCD, whose L2 does not see this one's.
+            store_coherent(pacc + idx, at);
+            if (d == 0) {
+                store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
+                store_coherent(pl + r, lt);
+            }
         } else {
             pacc[idx] = at;
             if (d == 0) {
-                pm[r] = mg * LN2;      // natural-log units, the reference's partial format
+                pm[r] = mg * LN2;
                 pl[r] = lt;
             }
         }
     }
-    if (single) return;
+    if (single || !a.fuse) return;
 
     // ---- the last group of this (b, h) to arrive merges all splits ----
-    __threadfence();
+    // The partials above bypass the non-coherent L2 path, so ordering needs
+    // only their completion before the arrival count: no whole-L2 writeback
+    // or invalidate (which a device-scope fence would issue in every group).
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     if (tid == 0) {
-        const int prev = atomicAdd(a.counters + bh, 1);
+        const int prev = __hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
         sm.is_last = prev == S - 1;
     }
     __syncthreads();
     if (!sm.is_last) return;
-    __threadfence();
-    combine_partials(a.part_acc + bh * S * (int64_t)NR * HEAD_DIM, a.part_m + bh * S * NR,
-                     a.part_l + bh * S * NR, S, NR, (int64_t)NR * HEAD_DIM, HEAD_DIM, NR,
-                     a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h, 0, a.so_r, tid, WAVE * NW);
-    if (tid == 0) atomicExch(a.counters + bh, 0);
+    static_assert(WAVE * NW == 256, "the fused combine is written for 256 threads");
+    combine_partials<1, true>(a.part_acc + bh * S * (int64_t)NR * HEAD_DIM, a.part_m + bh * S * NR,
+                              a.part_l + bh * S * NR, S, NR, (int64_t)NR * HEAD_DIM, HEAD_DIM, NR,
+                              a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h, 0, a.so_r, tid,
+                              sm.cmb);
+    if (tid == 0)
+        __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+template <int VEC>
 __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
+    __shared__ CombineSmem cs;
     const int bh = blockIdx.x;
     const int b = bh / p.H, h = bh % p.H;
-    combine_partials(p.acc + (int64_t)b * p.sa_b + (int64_t)h * p.sa_h,
-                     p.m + (int64_t)b * p.sm_b + (int64_t)h * p.sm_h,
-                     p.l + (int64_t)b * p.sm_b + (int64_t)h * p.sm_h, p.S, p.NR, p.sa_s, p.sa_r,
-                     p.sm_s,
-                     (char*)p.out + ((int64_t)b * p.so_b + (int64_t)h * p.so_h) * (p.out_f32 ? 4 : 2),
-                     p.out_f32, p.so_r, threadIdx.x, blockDim.x);
+    combine_partials<VEC>(p.acc + (int64_t)b * p.sa_b + (int64_t)h * p.sa_h,
+                          p.m + (int64_t)b * p.sm_b + (int64_t)h * p.sm_h,
+                          p.l + (int64_t)b * p.sm_b + (int64_t)h * p.sm_h, p.S, p.NR, p.sa_s,
+                          p.sa_r, p.sm_s,
+                          (char*)p.out + ((int64_t)b * p.so_b + (int64_t)h * p.so_h) *
+                                             (p.out_f32 ? 4 : 2),
+                          p.out_f32, p.so_r, threadIdx.x, cs);
 }
 
 // ------------------------------------------------------------- launch ----
@@ -489,7 +608,7 @@ static hipError_t launch_t(const DecodeParams& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_decode(const DecodeParams& a, hipStream_t stream) {
+static hipError_t launch_kernel(const DecodeParams& a, hipStream_t stream) {
     if (a.sel) return launch_t<KV_FP16, false, false, true>(a, stream);
     if (a.kind == KV_FP16) return launch_t<KV_FP16, false, false, false>(a, stream);
     const bool asym = a.k_zero != nullptr, res = a.k_res != nullptr;
@@ -499,8 +618,52 @@ hipError_t launch_decode(const DecodeParams& a, hipStream_t stream) {
     return launch_t<KV_INT8, false, false, false>(a, stream);
 }
 
+// LATENTSERVE_HIP_COMBINE=separate merges the splits in a second launch
+// instead of in the decode kernel's last-arriving group (for comparison).
+static bool fused_combine() {
+    static const int fused = [] {
+        const char* e = getenv("LATENTSERVE_HIP_COMBINE");
+        return (e && strcmp(e, "separate") == 0) ? 0 : 1;
+    }();
+    return fused != 0;
+}
+
+hipError_t launch_decode(const DecodeParams& a_in, hipStream_t stream) {
+    DecodeParams a = a_in;
+    a.fuse = fused_combine() ? 1 : 0;
+    hipError_t e = launch_kernel(a, stream);
+    if (e != hipSuccess || a.fuse || a.num_splits == 1) return e;
+    CombineParams p;
+    p.acc = a.part_acc;
+    p.sa_r = HEAD_DIM;
+    p.sa_s = (int64_t)a.NR * HEAD_DIM;
+    p.sa_h = p.sa_s * a.num_splits;
+    p.sa_b = p.sa_h * a.H;
+    p.m = a.part_m;
+    p.l = a.part_l;
+    p.sm_s = a.NR;
+    p.sm_h = (int64_t)a.NR * a.num_splits;
+    p.sm_b = p.sm_h * a.H;
+    p.out = a.out;
+    p.out_f32 = 0;
+    p.so_b = a.so_b;
+    p.so_h = a.so_h;
+    p.so_r = a.so_r;
+    p.B = a.B;
+    p.H = a.H;
+    p.S = a.num_splits;
+    p.NR = a.NR;
+    return launch_combine(p, stream);
+}
+
 hipError_t launch_combine(const CombineParams& p, hipStream_t stream) {
-    hipLaunchKernelGGL(combine_kernel, dim3(p.B * p.H), dim3(256), 0, stream, p);
+    // float4 partial loads when every row and split starts 16-byte aligned
+    const bool vec = ((uintptr_t)p.acc % 16 == 0) && p.sa_b % 4 == 0 && p.sa_h % 4 == 0 &&
+                     p.sa_s % 4 == 0 && p.sa_r % 4 == 0;
+    if (vec)
+        hipLaunchKernelGGL(combine_kernel<4>, dim3(p.B * p.H), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(combine_kernel<1>, dim3(p.B * p.H), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -29,6 +29,7 @@ MAX_NREP = 16
 # its split); must match NWAVES in csrc/ls_decode.hip.
 WAVES_PER_GROUP = 4
 MAX_SPLITS = 1024
+GROUPS_PER_CU = 2
 
 _CU_COUNT: dict = {}
 
@@ -44,13 +45,13 @@ def choose_splits(batch: int, kv_heads: int, num_pages: int,
                   device: Optional[torch.device] = None) -> int:
     """Splits per (sequence, KV head) for the MI355X kernel.
 
-    Enough workgroups for about three resident groups per CU (each group is
-    four waves streaming pages), but never so many that a wave gets fewer
-    than two pages. Fixed by (batch, heads, pages) alone, so a captured graph
-    can pin it per context bucket.
+    One resident wave of workgroups: GROUPS_PER_CU groups of four waves per
+    CU (the fp16 kernel's register budget allows two per CU), but never so
+    many splits that a wave gets fewer than two pages. Fixed by (batch,
+    heads, pages) alone, so a captured graph can pin it per context bucket.
     """
     cus = _cus(device) if device is not None and torch.cuda.is_available() else 256
-    target_groups = 3 * cus
+    target_groups = GROUPS_PER_CU * cus
     by_cus = -(-target_groups // max(1, batch * kv_heads))
     by_pages = max(1, num_pages // (2 * WAVES_PER_GROUP))
     return max(1, min(MAX_SPLITS, by_cus, by_pages))
