@@ -39,6 +39,8 @@ CONFIGS = {
     "c3": dict(batch=8, ctx=32768, kind="fp16", workload="fp16 paged decode B8 x 32768"),
     "c3r": dict(batch=16, ctx=32768, kind="fp16", ragged=True,
                 workload="fp16 paged decode B16 ragged L~U[512,32768]"),
+    # diagnostic: the same bytes as c2 in 512 short sequences (no split merge needed)
+    "flat": dict(batch=512, ctx=512, kind="fp16", workload="fp16 paged decode B512 x 512"),
     "c4": dict(batch=16, ctx=16384, kind="int8",
                workload="INT8 paged decode B16 x 16384 (fp32 scales, fp16 last-page K residual)"),
 }
@@ -52,6 +54,9 @@ def parse():
     p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     p.add_argument("--splits", type=int, default=None)
     p.add_argument("--layers", type=int, default=LAYERS)
+    p.add_argument("--tables", default="random", choices=["random", "contiguous"],
+                   help="block-table layout (contiguous: the pages of a sequence are adjacent, "
+                        "a diagnostic of the gather's cost)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seqs", type=int, default=None,
                    help="sequences in the CPU-baseline sample (default: the whole batch)")
@@ -90,7 +95,7 @@ def algorithmic_bytes(cfg, lens) -> int:
     return kv + q + out + tables
 
 
-def build_workload(cfg, layers, seed=0):
+def build_workload(cfg, layers, seed=0, contiguous=False):
     import numpy as np
     import torch
 
@@ -101,7 +106,10 @@ def build_workload(cfg, layers, seed=0):
     width = (cfg["ctx"] + PAGE - 1) // PAGE
     nb = b * width + 4
     g = torch.Generator(device=dev).manual_seed(seed)
-    tables = torch.randperm(nb, device=dev, generator=g)[: b * width].view(b, width)
+    if contiguous:
+        tables = torch.arange(b * width, device=dev).view(b, width)
+    else:
+        tables = torch.randperm(nb, device=dev, generator=g)[: b * width].view(b, width)
     tables = tables.to(torch.int32).contiguous()
     seq = torch.from_numpy(lens).to(dev)
     pools = []
@@ -216,7 +224,7 @@ def main():
         return
     cfg = CONFIGS[args.config]
     layers = max(1, args.layers)
-    tables, seq, pools, max_len = build_workload(cfg, layers)
+    tables, seq, pools, max_len = build_workload(cfg, layers, contiguous=args.tables == "contiguous")
     lens = seq.cpu().numpy()
     nbytes = algorithmic_bytes(cfg, lens)
     from latentserve_amd.kernels.hip import paged_decode_hip as pdh

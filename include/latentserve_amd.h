@@ -21,11 +21,17 @@
  *   k_residual  [R, 16, H_kv, 128] fp16           res_strides[3] = (row, token, head)
  *   res_rows    [B] int32 (row of k_residual holding each sequence's last page)
  *   out         [B, H_kv, n_rep, 128] fp16        out_strides[3] = (b, h, r)
- *   part_acc    fp32 [B, H_kv, num_splits, n_rep, 128]  contiguous scratch
- *   part_m/l    fp32 [B, H_kv, num_splits, n_rep]       contiguous scratch
- *   counters    int32 [B * H_kv], zero before the first call; every call
- *               leaves it zero again.  Calls that share scratch must be
- *               ordered on one stream.
+ *   workspace   fp32 scratch of ls_decode_workspace_bytes() bytes, 256-byte
+ *               aligned (one record per (b, h, split): acc[n_rep][128],
+ *               m[16], l[16]); needed only when num_splits > 1
+ *   counters    int32 [2 * B * H_kv], zero before the first call; every
+ *               call leaves it zero again (per (sequence, head): an arrival
+ *               count of split groups and a page-claim count).  Calls that
+ *               share scratch must be ordered on one stream.
+ *   max_seq_len the longest sequence in the call (the caller's bound, e.g.
+ *               a graph bucket); it sets the pages per split.  A sequence
+ *               longer than it is still handled (its split is re-derived on
+ *               the device, as the reference does); 0 = always derive.
  *
  * The reference (Jash-Vora/LatentServe) has no C ABI: its kernels are CuPy
  * launches of extern "C" __global__ functions with positional pointer and
@@ -54,20 +60,27 @@ const char* ls_last_error(void);
 /* ABI version (bumped on any signature change). */
 int ls_abi_version(void);
 
+/* Bytes of `workspace` a decode call with these sizes needs (0 when
+ * num_splits == 1).  No counterpart in the reference, which sizes its
+ * partial buffers in Python (kernels/gqa/paged_decode.py:783-787). */
+size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits);
+
 /* fp16 paged decode.  Replaces paged_decode_fp16 + the Triton combine, i.e.
  * paged_decode_cuda() for an fp16 pool (kernels/cuda/paged_decode_cuda.py:202-252,
  * kernels/cuda/paged_decode_fp16.cu:55-64) behind paged_decode_attention
- * (kernels/gqa/paged_decode.py:709-829).  Pages per split are derived on the
- * device from seq_lens (paged_decode_fp16.cu:79-83).  With num_splits == 1
- * the output is written directly and the part_* and counters buffers are not
- * touched (they may be NULL). */
+ * (kernels/gqa/paged_decode.py:709-829).  One launch: the splits are merged
+ * by the last workgroup of each (sequence, head) to finish.  Pages are
+ * claimed dynamically by every wave of every split of a (sequence, head),
+ * so the splits only set how many groups share the walk.  With
+ * num_splits == 1 the output is written directly and workspace is not
+ * touched (it may be NULL). */
 int ls_paged_decode_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
                          const void* v_pool, const int64_t* kv_strides, int num_blocks,
                          const int32_t* block_tables, int64_t bt_stride, int max_pages,
                          const int32_t* seq_lens, void* out, const int64_t* out_strides,
-                         float* part_acc, float* part_m, float* part_l, int32_t* counters,
+                         float* workspace, int32_t* counters,
                          int batch, int kv_heads, int n_rep, int head_dim, int page,
-                         int num_splits, float softmax_scale, void* stream);
+                         int num_splits, int max_seq_len, float softmax_scale, void* stream);
 
 /* INT8 paged decode.  Replaces paged_decode_int8 (kernels/cuda/paged_decode_int8.cu:87-102;
  * launcher kernels/cuda/paged_decode_cuda.py:236-244).  k_scale/v_scale
@@ -80,9 +93,9 @@ int ls_paged_decode_int8(const void* q, const int64_t* q_strides, const void* k_
                          const void* k_residual, const int64_t* res_strides, int res_capacity,
                          const int32_t* res_rows, const int32_t* block_tables, int64_t bt_stride,
                          int max_pages, const int32_t* seq_lens, void* out,
-                         const int64_t* out_strides, float* part_acc, float* part_m,
-                         float* part_l, int32_t* counters, int batch, int kv_heads, int n_rep,
-                         int head_dim, int page, int num_splits, float softmax_scale,
+                         const int64_t* out_strides, float* workspace,
+                         int32_t* counters, int batch, int kv_heads, int n_rep,
+                         int head_dim, int page, int num_splits, int max_seq_len, float softmax_scale,
                          void* stream);
 
 /* Page-subset (sparse) decode over sel[b, h, 0:n] logical pages, fp16 pool.
@@ -90,15 +103,16 @@ int ls_paged_decode_int8(const void* q, const int64_t* q_strides, const void* k_
  * sparse_decode, kernels/cuda/paged_sparse.py:185-219).  With ratio > 0 each
  * sequence attends its first max(recent+1, ceilf(ratio*pages)) entries, capped
  * at its pages and num_sel; ratio <= 0 attends all num_sel.  Entries outside
- * [0, pages) are skipped. */
+ * [0, pages) are skipped.  The list is split on the device; max_seq_len is
+ * not used. */
 int ls_paged_sparse_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
                          const void* v_pool, const int64_t* kv_strides, int num_blocks,
                          const int32_t* block_tables, int64_t bt_stride, int max_pages,
                          const int32_t* seq_lens, const int32_t* sel, const int64_t* sel_strides,
                          int num_sel, float ratio, int recent, void* out,
-                         const int64_t* out_strides, float* part_acc, float* part_m,
-                         float* part_l, int32_t* counters, int batch, int kv_heads, int n_rep,
-                         int head_dim, int page, int num_splits, float softmax_scale,
+                         const int64_t* out_strides, float* workspace,
+                         int32_t* counters, int batch, int kv_heads, int n_rep,
+                         int head_dim, int page, int num_splits, int max_seq_len, float softmax_scale,
                          void* stream);
 
 /* Merge split partials: combine_splits / _combine_kernel

@@ -29,17 +29,18 @@ LS_ERR_HIP = 2
 _SIGNATURES = {
     "ls_abi_version": [],
     "ls_last_error": [],
+    "ls_decode_workspace_bytes": [_I32, _I32, _I32, _I32],
     "ls_paged_decode_fp16": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
-        _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
+        _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
     "ls_paged_decode_int8": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64P, _VP, _I64P, _VP, _VP,
         _VP, _I64P, _I32, _VP, _VP, _I64, _I32, _VP, _VP, _I64P,
-        _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
+        _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
     "ls_paged_sparse_fp16": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
-        _I32, _F32, _I32, _VP, _I64P, _VP, _VP, _VP, _VP,
-        _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
+        _I32, _F32, _I32, _VP, _I64P, _VP, _VP,
+        _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
     "ls_combine_splits": [
         _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
 }
@@ -67,7 +68,8 @@ def lib() -> ctypes.CDLL:
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_char_p if name == "ls_last_error" else ctypes.c_int
+            fn.restype = {"ls_last_error": ctypes.c_char_p,
+                          "ls_decode_workspace_bytes": ctypes.c_size_t}.get(name, ctypes.c_int)
         _lib = handle
     return _lib
 

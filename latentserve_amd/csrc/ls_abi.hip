@@ -51,7 +51,7 @@ bool rows_aligned(const void* p, const int64_t* st, int count, size_t elem, size
 int check_common(const void* q, const int64_t* q_strides, const void* k_pool, const void* v_pool,
                  const int64_t* kv_strides, int num_blocks, const int32_t* block_tables,
                  int max_pages, const int32_t* seq_lens, void* out, const int64_t* out_strides,
-                 float* part_acc, float* part_m, float* part_l, int32_t* counters, int batch,
+                 float* workspace, int32_t* counters, int batch,
                  int kv_heads, int n_rep, int head_dim, int page, int num_splits, size_t kv_elem) {
     if (!q || !q_strides || !k_pool || !v_pool || !kv_strides || !block_tables || !seq_lens ||
         !out || !out_strides)
@@ -72,8 +72,11 @@ int check_common(const void* q, const int64_t* q_strides, const void* k_pool, co
         !rows_aligned(v_pool, kv_strides, 3, kv_elem, kv_elem == 2 ? 16 : 8))
         return fail(LS_ERR_INVALID, "K/V pool rows must be %d-byte aligned", kv_elem == 2 ? 16 : 8);
     if (!aligned(out, 2)) return fail(LS_ERR_INVALID, "out must be 2-byte aligned");
-    if (num_splits > 1 && (!part_acc || !part_m || !part_l || !counters))
-        return fail(LS_ERR_INVALID, "num_splits > 1 needs part_acc, part_m, part_l and counters");
+    if (!counters) return fail(LS_ERR_INVALID, "counters is required");
+    if (num_splits > 1 && !workspace)
+        return fail(LS_ERR_INVALID, "num_splits > 1 needs workspace");
+    if (num_splits > 1 && !aligned(workspace, 256))
+        return fail(LS_ERR_INVALID, "workspace must be 256-byte aligned");
     (void)out_strides;
     return LS_OK;
 }
@@ -81,9 +84,9 @@ int check_common(const void* q, const int64_t* q_strides, const void* k_pool, co
 void fill_common(ls::DecodeParams& a, const void* q, const int64_t* q_strides, const void* k_pool,
                  const void* v_pool, const int64_t* kv_strides, int num_blocks,
                  const int32_t* block_tables, int64_t bt_stride, int max_pages,
-                 const int32_t* seq_lens, void* out, const int64_t* out_strides, float* part_acc,
-                 float* part_m, float* part_l, int32_t* counters, int batch, int kv_heads,
-                 int n_rep, int num_splits, float softmax_scale) {
+                 const int32_t* seq_lens, void* out, const int64_t* out_strides, float* workspace,
+                 int32_t* counters, int batch, int kv_heads,
+                 int n_rep, int num_splits, int max_seq_len, float softmax_scale) {
     memset(&a, 0, sizeof a);
     a.q = (const _Float16*)q;
     a.sq_b = q_strides[0];
@@ -99,9 +102,12 @@ void fill_common(ls::DecodeParams& a, const void* q, const int64_t* q_strides, c
     a.max_pages = max_pages;
     a.num_blocks = num_blocks;
     a.seq_lens = seq_lens;
-    a.part_acc = part_acc;
-    a.part_m = part_m;
-    a.part_l = part_l;
+    a.work = workspace;
+    if (max_seq_len > 0) {
+        int pages = (max_seq_len + ls::PAGE - 1) / ls::PAGE;
+        pages = pages < max_pages ? pages : max_pages;
+        a.pages_per_split = (pages + num_splits - 1) / num_splits;
+    }
     a.counters = counters;
     a.out = (_Float16*)out;
     a.so_b = out_strides[0];
@@ -120,24 +126,30 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 1; }
+int ls_abi_version(void) { return 2; }
+
+size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
+    if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
+    const size_t rec = (size_t)n_rep * ls::HEAD_DIM + 2 * ls::MAX_NREP;
+    return (size_t)batch * kv_heads * num_splits * rec * sizeof(float);
+}
 
 int ls_paged_decode_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
                          const void* v_pool, const int64_t* kv_strides, int num_blocks,
                          const int32_t* block_tables, int64_t bt_stride, int max_pages,
                          const int32_t* seq_lens, void* out, const int64_t* out_strides,
-                         float* part_acc, float* part_m, float* part_l, int32_t* counters,
+                         float* workspace, int32_t* counters,
                          int batch, int kv_heads, int n_rep, int head_dim, int page,
-                         int num_splits, float softmax_scale, void* stream) {
+                         int num_splits, int max_seq_len, float softmax_scale, void* stream) {
     int rc = check_common(q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables,
-                          max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l,
+                          max_pages, seq_lens, out, out_strides, workspace,
                           counters, batch, kv_heads, n_rep, head_dim, page, num_splits, 2);
     if (rc) return rc;
     if (batch == 0) return LS_OK;
     ls::DecodeParams a;
     fill_common(a, q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables, bt_stride,
-                max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l, counters, batch,
-                kv_heads, n_rep, num_splits, softmax_scale);
+                max_pages, seq_lens, out, out_strides, workspace, counters, batch,
+                kv_heads, n_rep, num_splits, max_seq_len, softmax_scale);
     a.kind = ls::KV_FP16;
     return hip_status(ls::launch_decode(a, (hipStream_t)stream), "ls_paged_decode_fp16");
 }
@@ -149,12 +161,12 @@ int ls_paged_decode_int8(const void* q, const int64_t* q_strides, const void* k_
                          const void* k_residual, const int64_t* res_strides, int res_capacity,
                          const int32_t* res_rows, const int32_t* block_tables, int64_t bt_stride,
                          int max_pages, const int32_t* seq_lens, void* out,
-                         const int64_t* out_strides, float* part_acc, float* part_m,
-                         float* part_l, int32_t* counters, int batch, int kv_heads, int n_rep,
-                         int head_dim, int page, int num_splits, float softmax_scale,
+                         const int64_t* out_strides, float* workspace,
+                         int32_t* counters, int batch, int kv_heads, int n_rep,
+                         int head_dim, int page, int num_splits, int max_seq_len, float softmax_scale,
                          void* stream) {
     int rc = check_common(q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables,
-                          max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l,
+                          max_pages, seq_lens, out, out_strides, workspace,
                           counters, batch, kv_heads, n_rep, head_dim, page, num_splits, 1);
     if (rc) return rc;
     if (!k_scale || !ks_strides || !v_scale || !vs_strides)
@@ -178,8 +190,8 @@ int ls_paged_decode_int8(const void* q, const int64_t* q_strides, const void* k_
     if (batch == 0) return LS_OK;
     ls::DecodeParams a;
     fill_common(a, q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables, bt_stride,
-                max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l, counters, batch,
-                kv_heads, n_rep, num_splits, softmax_scale);
+                max_pages, seq_lens, out, out_strides, workspace, counters, batch,
+                kv_heads, n_rep, num_splits, max_seq_len, softmax_scale);
     a.kind = ls::KV_INT8;
     a.k_scale = k_scale;
     a.sks_b = ks_strides[0];
@@ -206,12 +218,12 @@ int ls_paged_sparse_fp16(const void* q, const int64_t* q_strides, const void* k_
                          const int32_t* block_tables, int64_t bt_stride, int max_pages,
                          const int32_t* seq_lens, const int32_t* sel, const int64_t* sel_strides,
                          int num_sel, float ratio, int recent, void* out,
-                         const int64_t* out_strides, float* part_acc, float* part_m,
-                         float* part_l, int32_t* counters, int batch, int kv_heads, int n_rep,
-                         int head_dim, int page, int num_splits, float softmax_scale,
+                         const int64_t* out_strides, float* workspace,
+                         int32_t* counters, int batch, int kv_heads, int n_rep,
+                         int head_dim, int page, int num_splits, int max_seq_len, float softmax_scale,
                          void* stream) {
     int rc = check_common(q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables,
-                          max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l,
+                          max_pages, seq_lens, out, out_strides, workspace,
                           counters, batch, kv_heads, n_rep, head_dim, page, num_splits, 2);
     if (rc) return rc;
     if (!sel || !sel_strides) return fail(LS_ERR_INVALID, "sparse decode needs sel");
@@ -219,8 +231,8 @@ int ls_paged_sparse_fp16(const void* q, const int64_t* q_strides, const void* k_
     if (batch == 0) return LS_OK;
     ls::DecodeParams a;
     fill_common(a, q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables, bt_stride,
-                max_pages, seq_lens, out, out_strides, part_acc, part_m, part_l, counters, batch,
-                kv_heads, n_rep, num_splits, softmax_scale);
+                max_pages, seq_lens, out, out_strides, workspace, counters, batch,
+                kv_heads, n_rep, num_splits, max_seq_len, softmax_scale);
     a.kind = ls::KV_FP16;
     a.sel = sel;
     a.ssel_b = sel_strides[0];

@@ -70,8 +70,10 @@ __device__ __forceinline__ h4 as_h4(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(h4, t);
 }
 
+// KV pages are read exactly once per call: non-temporal loads keep them from
+// displacing the block tables, queries and partials in the caches.
 template <typename T>
-__device__ __forceinline__ T ldg(const T* p) {
+__device__ __forceinline__ T stream_load(const T* p) {
     return __builtin_nontemporal_load(p);
 }
 

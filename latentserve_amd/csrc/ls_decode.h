@@ -36,9 +36,9 @@ struct DecodeParams {
     int num_sel;
     float ratio;
     int recent;
-    float* part_acc;                   // [B, H, S, NR, 128] contiguous
-    float* part_m;                     // [B, H, S, NR] contiguous, natural-log units
-    float* part_l;                     // [B, H, S, NR] contiguous
+    float* work;                       // [B, H, S] records of NR*128 + 32 floats:
+                                       // acc[NR][128], m[16] (natural log), l[16]
+    int pages_per_split;               // > 0: dense walk partition given by the host
     int32_t* counters;                 // [B * H], zero at rest, reset by the kernel
     _Float16* out;
     int64_t so_b, so_h, so_r;

@@ -51,25 +51,23 @@ namespace ls {
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 
-// LDS scratch of combine_partials.
-constexpr int CMB_CHUNK = 64;   // splits whose weights are staged at once
-struct CombineSmem {
-    float red[16][MAX_NREP];            // per-thread-group partial max / sum
-    float mg[MAX_NREP];                 // row max over all splits
-    float lt[MAX_NREP];                 // row sum of weighted l
-    float w[CMB_CHUNK][MAX_NREP];       // weights of the current chunk of splits
-};
-
-
-template <int NW>
+template <int NWT, int HG>
 struct DecodeSmem {
-    float m[NW][MAX_NREP];
-    float l[NW][MAX_NREP];
+    // During the walk the merge buffer holds the group's item table: the
+    // block of every page of its range (dense walk, shared by the heads) or,
+    // per head, the block and page of every list entry (page-subset walk).
+    // Rows of the wave states are padded by 16 bytes so that the 16 rows a
+    // wave writes at once fall in different banks.
+    static constexpr int ROW = HEAD_DIM + 4;
+    static constexpr int ENT_INTS = NWT * MAX_NREP * ROW;
+    float m[NWT][MAX_NREP];
+    float l[NWT][MAX_NREP];
     union {
-        float acc[NW][MAX_NREP][HEAD_DIM];   // wave states, merged once
-        CombineSmem cmb;                     // then reused by the split combine
+        int ent[ENT_INTS];
+        float acc[NWT][MAX_NREP][ROW];            // after it: one head's wave states
     };
-    int is_last;
+    int is_last[HG];
+    int claim;
 };
 
 // Registers of one page for one wave.  K/V as raw dwords; INT8 rows are half
@@ -92,15 +90,15 @@ __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, i
         const half_t* kp = (const half_t*)a.k_pool + base + (int64_t)c * a.sk_p + 8 * g;
         const half_t* vp = (const half_t*)a.v_pool + base + (int64_t)(4 * g) * a.sk_p + 8 * c;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) buf.k[j] = *(const u4*)(kp + 32 * j);
+        for (int j = 0; j < 4; ++j) buf.k[j] = stream_load((const u4*)(kp + 32 * j));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) buf.v[i] = *(const u4*)(vp + (int64_t)i * a.sk_p);
+        for (int i = 0; i < 4; ++i) buf.v[i] = stream_load((const u4*)(vp + (int64_t)i * a.sk_p));
     } else {
         buf.res = HAS_RES && page == num_pages - 1;
         const int8_t* vp = (const int8_t*)a.v_pool + base + (int64_t)(4 * g) * a.sk_p + 8 * c;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const u2 t = *(const u2*)(vp + (int64_t)i * a.sk_p);
+            const u2 t = stream_load((const u2*)(vp + (int64_t)i * a.sk_p));
             buf.v[i].x = t.x;
             buf.v[i].y = t.y;
         }
@@ -123,7 +121,7 @@ __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, i
             const int8_t* kp = (const int8_t*)a.k_pool + base + (int64_t)c * a.sk_p + 8 * g;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const u2 t = *(const u2*)(kp + 32 * j);
+                const u2 t = stream_load((const u2*)(kp + 32 * j));
                 buf.k[j].x = t.x;
                 buf.k[j].y = t.y;
             }
@@ -198,7 +196,8 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
     float mloc = neg_inf();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        x[i] = tok0 + i < len ? (s[i] + qz) * scale_log2 : neg_inf();
+        // unsigned: a dead item (page -1, len 0) masks every token
+        x[i] = (unsigned)(tok0 + i) < (unsigned)len ? (s[i] + qz) * scale_log2 : neg_inf();
         mloc = fmaxf(mloc, x[i]);
     }
     const float m_new = fmaxf(st.m, group4_max(mloc));
@@ -263,125 +262,134 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
 }
 
 // Merge S partial states of one (b, h) into out: combine_splits
-// (kernels/gqa/paged_decode.py:689-706).  256 threads.  Thread t owns row
-// r = t & 15 of split group t >> 4 for the weight passes, and float4 columns
-// of the output for the accumulation; every global load of a pass is issued
-// before any is consumed, so a pass costs one memory round trip rather than
-// one per split.
+// (kernels/gqa/paged_decode.py:689-706).  256 threads; thread t owns four
+// adjacent channels of one row.  Splits are taken 16 at a time with every
+// load of a chunk issued before any is used (one memory round trip per
+// chunk), and the chunks are merged by a running max (the same rescale the
+// page loop applies).  VEC 4 reads the channels as one 16-byte load (rows
+// and splits 16-byte aligned), VEC 1 as four scalar loads.
+constexpr int CMB_CHUNK = 16;
+
 __device__ __forceinline__ void store_coherent(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-template <bool COH>
-__device__ __forceinline__ float load_part(const float* p) {
-    if (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return *p;
-}
 
-template <int VEC, bool COH = false>
+template <int VEC>
 __device__ void combine_partials(const float* acc, const float* m, const float* l, int S, int NR,
                                  int64_t sa_s, int64_t sa_r, int64_t sm_s, void* out, int out_f32,
-                                 int64_t so_r, int tid, CombineSmem& cs) {
-    const int r = tid & 15, grp = tid >> 4;
-    const bool row_ok = r < NR;
-    // pass 1: row max
-    float mx = neg_inf();
-    if (row_ok)
-        for (int s = grp; s < S; s += 16) mx = fmaxf(mx, load_part<COH>(m + s * sm_s + r));
-    cs.red[grp][r] = mx;
-    __syncthreads();
-    if (tid < MAX_NREP) {
-        float v = neg_inf();
+                                 int64_t so_r, int tid) {
+    for (int o = tid; o < NR * (HEAD_DIM / 4); o += 256) {
+        const int r = o / (HEAD_DIM / 4), d0 = (o % (HEAD_DIM / 4)) * 4;
+        float mg = neg_inf(), lt = 0.f;
+        float at[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < S; s0 += CMB_CHUNK) {
+            const int n = S - s0 < CMB_CHUNK ? S - s0 : CMB_CHUNK;
+            float mv[CMB_CHUNK], lv[CMB_CHUNK], av[CMB_CHUNK][4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v = fmaxf(v, cs.red[i][tid]);
-        cs.mg[tid] = v;
-    }
-    __syncthreads();
-    const float mgr = cs.mg[r];
-    const bool dead = mgr == neg_inf();
-
-    // pass 2: weights chunk by chunk, accumulating the output columns
-    constexpr int NV = HEAD_DIM / VEC;                        // vectors per row
-    constexpr int MAXO = (MAX_NREP * NV + 255) / 256;         // outputs per thread
-    const int n_out = NR * NV;
-    f4 accv[MAXO];
+            for (int i = 0; i < CMB_CHUNK; ++i) {
+                mv[i] = neg_inf();
+                lv[i] = 0.f;
 #pragma unroll
-    for (int i = 0; i < MAXO; ++i) accv[i] = (f4){0.f, 0.f, 0.f, 0.f};
-    float lsum = 0.f;
-    for (int s0 = 0; s0 < S; s0 += CMB_CHUNK) {
-        const int n = S - s0 < CMB_CHUNK ? S - s0 : CMB_CHUNK;
-        for (int i = grp; i < n; i += 16) {
-            float w = 0.f;
-            if (row_ok && !dead) {
-                w = __expf(load_part<COH>(m + (s0 + i) * sm_s + r) - mgr);
-                lsum += load_part<COH>(l + (s0 + i) * sm_s + r) * w;
-            }
-            cs.w[i][r] = w;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int oi = 0; oi < MAXO; ++oi) {
-            const int o = tid + 256 * oi;
-            if (o < n_out) {
-                const int orow = o / NV, col = (o % NV) * VEC;
-                const float* src = acc + (int64_t)s0 * sa_s + orow * sa_r + col;
-                f4 a4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 16
-                for (int i = 0; i < n; ++i) {
-                    const float w = cs.w[i][orow];
+                for (int e = 0; e < 4; ++e) av[i][e] = 0.f;
+                if (i < n) {
+                    const int64_t sp = (int64_t)(s0 + i);
+                    mv[i] = m[sp * sm_s + r];
+                    lv[i] = l[sp * sm_s + r];
+                    const float* src = acc + sp * sa_s + r * sa_r + d0;
                     if (VEC == 4) {
-                        a4 += w * *(const f4*)(src + i * sa_s);
+                        const f4 t = *(const f4*)src;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) av[i][e] = t[e];
                     } else {
-                        a4[0] += w * load_part<COH>(src + i * sa_s);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) av[i][e] = src[e];
                     }
                 }
-                accv[oi] += a4;
             }
+            float cm = mg;
+#pragma unroll
+            for (int i = 0; i < CMB_CHUNK; ++i) cm = fmaxf(cm, mv[i]);
+            if (cm == neg_inf()) continue;            // nothing valid yet
+            const float sc = __expf(mg - cm);          // 0 while mg is -inf
+            lt *= sc;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) at[e] *= sc;
+#pragma unroll
+            for (int i = 0; i < CMB_CHUNK; ++i) {
+                const float w = __expf(mv[i] - cm);    // 0 for empty splits (m = -inf)
+                lt += lv[i] * w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) at[e] += av[i][e] * w;
+            }
+            mg = cm;
         }
-        __syncthreads();
-    }
-    // row sums of the weighted l
-    cs.red[grp][r] = lsum;
-    __syncthreads();
-    if (tid < MAX_NREP) {
-        float v = 0.f;
+        const float inv = 1.f / fmaxf(lt, 1e-20f);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v += cs.red[i][tid];
-        cs.lt[tid] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int oi = 0; oi < MAXO; ++oi) {
-        const int o = tid + 256 * oi;
-        if (o < n_out) {
-            const int orow = o / NV, col = (o % NV) * VEC;
-            const float inv = 1.f / fmaxf(cs.lt[orow], 1e-20f);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                const float v = accv[oi][e] * inv;
-                if (out_f32)
-                    ((float*)out)[orow * so_r + col + e] = v;
-                else
-                    ((half_t*)out)[orow * so_r + col + e] = (half_t)v;
-            }
+        for (int e = 0; e < 4; ++e) {
+            const float v = at[e] * inv;
+            if (out_f32)
+                ((float*)out)[r * so_r + d0 + e] = v;
+            else
+                ((half_t*)out)[r * so_r + d0 + e] = (half_t)v;
         }
     }
 }
 
-template <int KIND, bool ASYM, bool HAS_RES, bool SPARSE, int NW>
-__global__ __launch_bounds__(WAVE* NW) void paged_decode_kernel(const DecodeParams a) {
+// Diagnostic: the page walk and every load, with the arithmetic replaced by
+// a fold of the loaded words (the loads-only ceiling of the access pattern).
+__device__ __forceinline__ void consume_page(const PageBuf& buf, WaveState& st) {
+    uint32_t x = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x ^= buf.k[j].x ^ buf.k[j].y ^ buf.k[j].z ^ buf.k[j].w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x ^= buf.v[i].x ^ buf.v[i].y ^ buf.v[i].z ^ buf.v[i].w;
+    st.acc[0][0] += __builtin_bit_cast(float, x & 0x3f8fffffu);
+    st.m = 0.f;
+}
+
+// Claim the next item of the group for the calling wave: an LDS atomic by
+// lane 0.  The result stays in lane 0's register until claimed_item()
+// reads it one iteration later, off the critical path.
+__device__ __forceinline__ int claim_item(int* counter, int lane) {
+    int r = 0;
+    if (lane == 0)
+        r = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return r;
+}
+__device__ __forceinline__ int claimed_item(int raw) { return __builtin_amdgcn_readlane(raw, 0); }
+
+template <int KIND, bool ASYM, bool HAS_RES, bool SPARSE, int NWT, int HG, int ABL = 0>
+__global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodeParams a) {
     // Pages in flight ahead of the one being computed: the fp16 page buffer
     // is 32 VGPRs, the INT8 one (codes + K scales) as large again.
     constexpr int PF_DEPTH = KIND == KV_FP16 ? 2 : 1;
-    __shared__ DecodeSmem<NW> sm;
+    constexpr int NB = PF_DEPTH + 1;
+    __shared__ DecodeSmem<NWT, HG> sm;
     const int H = a.H;
-    const int h = blockIdx.x % H;
-    const int split = blockIdx.x / H;
+    // A group serves HG adjacent KV heads of one (sequence, split) with NWT
+    // waves.  Its work items are (page, head) pairs, claimed one at a time
+    // from an LDS counter by whichever wave is ready: the oldest waves win
+    // memory arbitration and would otherwise finish a static share early
+    // and idle while the youngest finish theirs.
+    const int n_hg = H / HG;
+    const int wv = threadIdx.x / WAVE;
+    const int lane = threadIdx.x % WAVE;
+    const int h0 = (blockIdx.x % n_hg) * HG;
+    const int split = blockIdx.x / n_hg;
     const int b = blockIdx.y;
-    const int tid = threadIdx.x;
-    const int w = tid / WAVE;
-    const int lane = tid % WAVE;
     const int g = lane >> 4, c = lane & 15;
     const int S = a.num_splits;
+    if (threadIdx.x == 0) sm.claim = NB * NWT;      // items below were assigned statically
+
+    // Dense walk with pages-per-split given by the host (from the caller's
+    // max_seq_len): the group's block ids are requested before the sequence
+    // length arrives.  Any partition of the pages gives the same result
+    // (split-K is exact), so the host's only affects speed.
+    const bool host_split = !SPARSE && a.pages_per_split > 0;
+    int spec_blk = -1;
+    const int spec_lo = host_split ? split * a.pages_per_split : 0;
+    if (host_split && (int)threadIdx.x < a.pages_per_split && spec_lo + (int)threadIdx.x < a.max_pages)
+        spec_blk = a.block_tables[(int64_t)b * a.sbt_b + spec_lo + threadIdx.x];
 
     const int len = a.seq_lens[b];
     int num_pages = (len + PAGE - 1) / PAGE;
@@ -392,11 +400,10 @@ __global__ __launch_bounds__(WAVE* NW) void paged_decode_kernel(const DecodePara
         res_ok = rr >= 0 && rr < a.res_cap;
     }
 
-    // This split's slice of the page walk (dense) or of the selection list.
+    // The walk: the sequence's pages (dense) or its selection list (page
+    // subset, one list per head, all of the same length).
     int n_list = num_pages;
-    const int32_t* sel = nullptr;
     if (SPARSE) {
-        sel = a.sel + (int64_t)b * a.ssel_b + (int64_t)h * a.ssel_h;
         n_list = a.num_sel;
         if (a.ratio > 0.f) {
             int want;
@@ -410,206 +417,354 @@ __global__ __launch_bounds__(WAVE* NW) void paged_decode_kernel(const DecodePara
             n_list = want < a.num_sel ? want : a.num_sel;
         }
     }
-    const int per = (n_list + S - 1) / S;
-    const int lo = split * per;
+    // Pages per split: the host's when it covers this sequence, else derived
+    // here from the length (kernels/gqa/paged_decode.py:564-568).
+    const bool spec_ok = host_split && num_pages <= S * a.pages_per_split;
+    const int per = spec_ok ? a.pages_per_split : (n_list + S - 1) / S;
+    const int lo = spec_ok ? spec_lo : split * per;
     const int hi = lo + per < n_list ? lo + per : n_list;
+    const int n_ent = hi > lo ? hi - lo : 0;
+    const int n_items = n_ent * HG;
 
-    // Query operand: row c (zero beyond n_rep), channels 32j+8g..+8.
-    h4 qh[8];
-    float qf[4][8];
-    {
+    // Resolve the group's entries to (block, page) once, into LDS (the merge
+    // buffer, idle until the walk ends).  Block ids outside the pool, list
+    // entries outside the sequence and a last page whose residual row is
+    // outside the residual become -1 and are never dereferenced.  A range
+    // longer than the table resolves each claimed item from global memory.
+    constexpr int ENT_INTS = DecodeSmem<NWT, HG>::ENT_INTS;
+    constexpr int CAP = SPARSE ? ENT_INTS / (2 * HG) : ENT_INTS;
+    const bool cached = n_ent <= CAP;
+    auto resolve_global = [&](int e, int hh, int& blk, int& pg) {
+        pg = SPARSE ? a.sel[(int64_t)b * a.ssel_b + (int64_t)(h0 + hh) * a.ssel_h + lo + e] : lo + e;
+        blk = -1;
+        if (pg >= 0 && pg < num_pages) {
+            blk = a.block_tables[(int64_t)b * a.sbt_b + pg];
+            if (blk < 0 || blk >= a.num_blocks) blk = -1;
+            if (HAS_RES && pg == num_pages - 1 && !res_ok) blk = -1;
+        }
+    };
+    if (cached) {
+        if (SPARSE) {
+            for (int i = threadIdx.x; i < n_ent * HG; i += WAVE * NWT) {
+                const int hh = i / n_ent, e = i % n_ent;
+                int blk, pg;
+                resolve_global(e, hh, blk, pg);
+                sm.ent[(hh * 2) * CAP + e] = blk;
+                sm.ent[(hh * 2 + 1) * CAP + e] = pg;
+            }
+        } else {
+            for (int e = threadIdx.x; e < n_ent; e += WAVE * NWT) {
+                // this thread's speculative load covered entry threadIdx.x only
+                int blk = e == (int)threadIdx.x && spec_ok ? spec_blk : -2;
+                const int pg = lo + e;
+                if (blk == -2 || !(pg >= 0 && pg < num_pages)) {
+                    int p2;
+                    resolve_global(e, 0, blk, p2);
+                } else {
+                    if (blk < 0 || blk >= a.num_blocks) blk = -1;
+                    if (HAS_RES && pg == num_pages - 1 && !res_ok) blk = -1;
+                }
+                sm.ent[e] = blk;
+            }
+        }
+    }
+
+    // Query operands of the group's heads: row c (zero beyond n_rep),
+    // channels 32j+8g..+8.
+    h4 qh[HG][8];
+    float qf[HG][4][8];
+#pragma unroll
+    for (int hh = 0; hh < HG; ++hh) {
         const bool row_ok = c < a.NR;
-        const half_t* qp = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)c * a.sq_r + 8 * g;
+        const half_t* qp =
+            a.q + (int64_t)b * a.sq_b + (int64_t)(h0 + hh) * a.sq_h + (int64_t)c * a.sq_r + 8 * g;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             u4 t = {0u, 0u, 0u, 0u};
             if (row_ok) t = *(const u4*)(qp + 32 * j);
-            qh[2 * j] = as_h4(t.x, t.y);
-            qh[2 * j + 1] = as_h4(t.z, t.w);
+            qh[hh][2 * j] = as_h4(t.x, t.y);
+            qh[hh][2 * j + 1] = as_h4(t.z, t.w);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                qf[j][e] = (float)qh[2 * j][e];
-                qf[j][4 + e] = (float)qh[2 * j + 1][e];
+                qf[hh][j][e] = (float)qh[hh][2 * j][e];
+                qf[hh][j][4 + e] = (float)qh[hh][2 * j + 1][e];
             }
         }
     }
     const float scale_log2 = a.scale * LOG2E;
 
-    WaveState st;
+    WaveState st[HG];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) st.acc[t] = (f4){0.f, 0.f, 0.f, 0.f};
-    st.m = neg_inf();
-    st.l = 0.f;
-    st.z = 0.f;
-
-    // Wave w walks entries lo+w, lo+w+NW, ... in chunks of 64: lane i of the
-    // chunk resolves entry i to (logical page, physical block) once, and the
-    // page loop reads them back with readlane (no per-page table latency).
-    const int first = lo + w;
-    const int count = first < hi ? (hi - first + NW - 1) / NW : 0;
-    for (int base = 0; base < count; base += WAVE) {
-        const int n_chunk = count - base < WAVE ? count - base : WAVE;
-        int pg = -1, blk = 0;
-        if (lane < n_chunk) {
-            const int e = first + (base + lane) * NW;
-            pg = SPARSE ? sel[e] : e;
-            if (pg >= 0 && pg < num_pages) {
-                blk = a.block_tables[(int64_t)b * a.sbt_b + pg];
-                // Ids outside the pool, and a last page whose residual row is
-                // outside the residual, are never dereferenced.
-                if (blk < 0 || blk >= a.num_blocks) pg = -1;
-                if (HAS_RES && pg == num_pages - 1 && !res_ok) pg = -1;
-            } else {
-                pg = -1;
-            }
-        }
-        // Compact the valid entries to the front (a page-subset list pads
-        // short sequences with pages past their end, paged_sparse_fp16.cu:266).
-        const uint64_t mask = __ballot(pg >= 0);
-        const int n_valid = __popcll(mask);
-        if (mask != ~0ull) {
-            const int before = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
-            const int dst = pg >= 0 ? before : n_valid + (lane - before);
-            pg = __builtin_amdgcn_ds_permute(dst << 2, pg);
-            blk = __builtin_amdgcn_ds_permute(dst << 2, blk);
-        }
-        if (n_valid == 0) continue;
-
-        // Three page buffers in rotation: pages k+1 and k+2 are in flight
-        // while page k is computed.  Prefetches past the end re-read the
-        // last page (a cache hit) so every iteration waits the same way.
-        PageBuf buf[PF_DEPTH + 1];
-        const int last = n_valid - 1;
+    for (int hh = 0; hh < HG; ++hh) {
 #pragma unroll
-        for (int u = 0; u < PF_DEPTH; ++u) {
-            const int kk = u < last ? u : last;
-            load_page<KIND, ASYM, HAS_RES>(a, buf[u], __builtin_amdgcn_readlane(blk, kk),
-                                           __builtin_amdgcn_readlane(pg, kk), num_pages, b, h, g, c);
-        }
-        for (int k = 0; k < n_valid;) {
-#pragma unroll
-            for (int u = 0; u <= PF_DEPTH; ++u) {
-                const int kn = k + PF_DEPTH < last ? k + PF_DEPTH : last;
-                load_page<KIND, ASYM, HAS_RES>(a, buf[(u + PF_DEPTH) % (PF_DEPTH + 1)],
-                                               __builtin_amdgcn_readlane(blk, kn),
-                                               __builtin_amdgcn_readlane(pg, kn), num_pages, b, h,
-                                               g, c);
-                compute_page<KIND, ASYM>(buf[u], st, qh, qf, __builtin_amdgcn_readlane(pg, k), len,
-                                         scale_log2, g);
-                if (++k >= n_valid) break;
-            }
-        }
+        for (int t = 0; t < 8; ++t) st[hh].acc[t] = (f4){0.f, 0.f, 0.f, 0.f};
+        st[hh].m = neg_inf();
+        st[hh].l = 0.f;
+        st[hh].z = 0.f;
     }
-
-    // ---- merge the NW waves in LDS ----
-    const float lrow = group4_sum(st.l);
-    if (ASYM) {
-        const float zrow = group4_sum(st.z);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) st.acc[t] += zrow;
-    }
-    if (g == 0) {
-        sm.m[w][c] = st.m;
-        sm.l[w][c] = lrow;
-    }
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sm.acc[w][c][32 * g + 8 * i + t] = st.acc[t][i];
     __syncthreads();
+
+    // Item i: entry i / HG of head i % HG (the heads of a page are adjacent
+    // items, so a page's token rows are requested whole at about one time).
+    // Items past the end or unresolvable come back with blk -1: their buffer
+    // is filled from block 0 (any valid address: it keeps every iteration's
+    // loads and waits identical) and computed with every token masked.
+    auto resolve_lds = [&](int i, int& blk, int& pg, int& hh) {
+        hh = HG == 1 ? 0 : i % HG;
+        const int e = HG == 1 ? i : i / HG;
+        if (i >= n_items) {
+            blk = -1;
+            pg = -1;
+        } else if (SPARSE) {
+            blk = sm.ent[(hh * 2) * CAP + e];
+            pg = sm.ent[(hh * 2 + 1) * CAP + e];
+        } else {
+            blk = sm.ent[e];
+            pg = lo + e;
+        }
+    };
+    auto resolve_mem = [&](int i, int& blk, int& pg, int& hh) {
+        hh = HG == 1 ? 0 : i % HG;
+        const int e = HG == 1 ? i : i / HG;
+        if (i >= n_items) {
+            blk = -1;
+            pg = -1;
+        } else {
+            resolve_global(e, hh, blk, pg);
+        }
+    };
+
+    // Three page buffers in rotation: items k+1 and k+2 are in flight while
+    // item k is computed, and the item after is being claimed.
+    auto walk = [&](auto resolve) {
+        PageBuf buf[NB];
+        int item[NB], pgs[NB], ok[NB], hds[NB];
+        auto issue = [&](int slot, int it) {
+            int blk, pg, hh;
+            item[slot] = it;
+            resolve(it, blk, pg, hh);
+            ok[slot] = blk >= 0;
+            pgs[slot] = pg;
+            hds[slot] = hh;
+            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], ok[slot] ? blk : 0, ok[slot] ? pg : -1,
+                                           num_pages, b, h0 + hh, g, c);
+        };
+#pragma unroll
+        for (int u = 0; u < PF_DEPTH; ++u) issue(u, wv + u * NWT);
+        int it_n = wv + PF_DEPTH * NWT;
+        if (item[0] >= n_items) return;
+        while (true) {
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                // claim an item (read next iteration), then load the item
+                // claimed last iteration into the free buffer
+                const int raw_new = claim_item(&sm.claim, lane);
+                issue((u + PF_DEPTH) % NB, it_n);
+                it_n = claimed_item(raw_new);
+                // computed even when dead (every token masked, a no-op on the
+                // state): a skipped buffer would leave its loads unwaited and
+                // force conservative waits on the next reuse of its registers
+                const int live_len = ok[u] ? len : 0;
+#pragma unroll
+                for (int hh = 0; hh < HG; ++hh) {
+                    if (hds[u] == hh) {
+                        if (ABL == 1 || ABL == 2)
+                            consume_page(buf[u], st[hh]);
+                        else
+                            compute_page<KIND, ASYM>(buf[u], st[hh], qh[hh], qf[hh], pgs[u],
+                                                     live_len, scale_log2, g);
+                    }
+                }
+                // items arrive in increasing order: past the end, all later are too
+                if (item[(u + 1) % NB] >= n_items) return;
+            }
+        }
+    };
+    if (cached)
+        walk(resolve_lds);
+    else
+        walk(resolve_mem);
 
     const int NR = a.NR;
     const bool single = S == 1;
-    const int64_t bh = (int64_t)b * H + h;
-    float* pacc = a.part_acc + (bh * S + split) * (int64_t)NR * HEAD_DIM;
-    float* pm = a.part_m + (bh * S + split) * NR;
-    float* pl = a.part_l + (bh * S + split) * NR;
-    for (int idx = tid; idx < NR * HEAD_DIM; idx += WAVE * NW) {
-        const int r = idx / HEAD_DIM, d = idx % HEAD_DIM;
-        float mg = neg_inf();
+    if (ABL >= 2) {                      // diagnostic: no merge, no partials
 #pragma unroll
-        for (int u = 0; u < NW; ++u) mg = fmaxf(mg, sm.m[u][r]);
-        float lt = 0.f, at = 0.f;
-#pragma unroll
-        for (int u = 0; u < NW; ++u) {
-            const float wt = mg == neg_inf() ? 0.f : fast_exp2(sm.m[u][r] - mg);
-            lt += sm.l[u][r] * wt;
-            at += sm.acc[u][r][d] * wt;
+        for (int hh = 0; hh < HG; ++hh)
+            if (st[hh].acc[0][0] == 12345.f && st[hh].l == 1.f) a.out[threadIdx.x] = (half_t)st[hh].m;
+        __syncthreads();
+        if (!single && threadIdx.x < (unsigned)HG) {
+            const int64_t bh = (int64_t)b * H + h0 + threadIdx.x;
+            if (__hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == S - 1)
+                __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        if (single) {
-            a.out[(int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)r * a.so_r + d] =
-                (half_t)(at / fmaxf(lt, 1e-20f));
-        } else if (a.fuse) {
-            // Device-coherent (write-through) stores: the group that merges
-            // may run on another XCD, whose L2 does not see this one's.
-            store_coherent(pacc + idx, at);
-            if (d == 0) {
-                store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
-                store_coherent(pl + r, lt);
+        return;
+    }
+
+    // ---- merge the waves' states in LDS, one head at a time ----
+    // One record per (b, h, split): acc[NR][128], m[16], l[16].  Every cache
+    // line of a record is written by this group alone.
+    const int64_t rec = (int64_t)NR * HEAD_DIM + 2 * MAX_NREP;
+#pragma unroll
+    for (int hh = 0; hh < HG; ++hh) {
+        const float lrow = group4_sum(st[hh].l);
+        if (ASYM) {
+            const float zrow = group4_sum(st[hh].z);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) st[hh].acc[t] += zrow;
+        }
+        __syncthreads();                 // the table (or the previous head) is dead
+        if (g == 0) {
+            sm.m[wv][c] = st[hh].m;
+            sm.l[wv][c] = lrow;
+        }
+        // the lane's 32 channels 32g..32g+31 (channel 32g + 8i + t is element
+        // i of tile t) as eight 16-byte stores
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            f4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = st[hh].acc[4 * (j % 2) + e][j / 2];
+            *(f4*)&sm.acc[wv][c][32 * g + 4 * j] = v;
+        }
+        __syncthreads();
+
+        const int64_t bh = (int64_t)b * H + h0 + hh;
+        float* pacc = a.work + (bh * S + split) * rec;
+        float* pm = pacc + NR * HEAD_DIM;
+        float* pl = pm + MAX_NREP;
+        for (int idx = threadIdx.x; idx < NR * HEAD_DIM; idx += WAVE * NWT) {
+            const int r = idx / HEAD_DIM, d = idx % HEAD_DIM;
+            float mg = neg_inf();
+#pragma unroll
+            for (int u = 0; u < NWT; ++u) mg = fmaxf(mg, sm.m[u][r]);
+            float lt = 0.f, at = 0.f;
+#pragma unroll
+            for (int u = 0; u < NWT; ++u) {
+                const float wt = mg == neg_inf() ? 0.f : fast_exp2(sm.m[u][r] - mg);
+                lt += sm.l[u][r] * wt;
+                at += sm.acc[u][r][d] * wt;
             }
-        } else {
-            pacc[idx] = at;
-            if (d == 0) {
-                pm[r] = mg * LN2;
-                pl[r] = lt;
+            if (single) {
+                a.out[(int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h + (int64_t)r * a.so_r + d] =
+                    (half_t)(at / fmaxf(lt, 1e-20f));
+            } else if (a.fuse) {
+                // Device-coherent (write-through) stores: the group that merges
+                // may run on another XCD, whose L2 does not see this one's.
+                store_coherent(pacc + idx, at);
+                if (d == 0) {
+                    store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
+                    store_coherent(pl + r, lt);
+                }
+            } else {
+                pacc[idx] = at;
+                if (d == 0) {
+                    pm[r] = mg * LN2;
+                    pl[r] = lt;
+                }
             }
         }
     }
-    if (single || !a.fuse) return;
+    if (single) return;
 
-    // ---- the last group of this (b, h) to arrive merges all splits ----
-    // The partials above bypass the non-coherent L2 path, so ordering needs
+    // ---- the last group of each (b, h) to arrive merges all splits ----
+    // The records above bypass the non-coherent L2 path, so ordering needs
     // only their completion before the arrival count: no whole-L2 writeback
     // or invalidate (which a device-scope fence would issue in every group).
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    if (tid == 0) {
-        const int prev = __hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-        sm.is_last = prev == S - 1;
+    if (a.fuse) {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
     __syncthreads();
-    if (!sm.is_last) return;
-    static_assert(WAVE * NW == 256, "the fused combine is written for 256 threads");
-    combine_partials<1, true>(a.part_acc + bh * S * (int64_t)NR * HEAD_DIM, a.part_m + bh * S * NR,
-                              a.part_l + bh * S * NR, S, NR, (int64_t)NR * HEAD_DIM, HEAD_DIM, NR,
-                              a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h, 0, a.so_r, tid,
-                              sm.cmb);
-    if (tid == 0)
+    if (threadIdx.x < (unsigned)HG) {
+        const int64_t bh = (int64_t)b * H + h0 + threadIdx.x;
+        const int prev = __hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+        sm.is_last[threadIdx.x] = prev == S - 1;
+    }
+    __syncthreads();
+    // 256 threads per head: a group of HG heads merges each head it closed
+    static_assert(WAVE * NWT == 256 * HG, "the fused combine is written for 256 threads a head");
+    const int hh = threadIdx.x / 256, t256 = threadIdx.x % 256;
+    if (!sm.is_last[hh]) return;
+    const int64_t bh = (int64_t)b * H + h0 + hh;
+    if (a.fuse) {
+        // The records were written through to memory and no group has read
+        // their lines in this launch, so plain vector loads see them.
+        const float* recs = a.work + bh * S * rec;
+        combine_partials<4>(recs, recs + NR * HEAD_DIM, recs + NR * HEAD_DIM + MAX_NREP, S, NR,
+                            rec, HEAD_DIM, rec,
+                            a.out + (int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h, 0, a.so_r,
+                            t256);
+    }
+    // every group of this (b, h) has arrived: back to zero for the next launch
+    if (t256 == 0)
         __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int VEC>
 __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
-    __shared__ CombineSmem cs;
     const int bh = blockIdx.x;
     const int b = bh / p.H, h = bh % p.H;
     combine_partials<VEC>(p.acc + (int64_t)b * p.sa_b + (int64_t)h * p.sa_h,
-                          p.m + (int64_t)b * p.sm_b + (int64_t)h * p.sm_h,
-                          p.l + (int64_t)b * p.sm_b + (int64_t)h * p.sm_h, p.S, p.NR, p.sa_s,
-                          p.sa_r, p.sm_s,
-                          (char*)p.out + ((int64_t)b * p.so_b + (int64_t)h * p.so_h) *
-                                             (p.out_f32 ? 4 : 2),
-                          p.out_f32, p.so_r, threadIdx.x, cs);
+                            p.m + (int64_t)b * p.sm_b + (int64_t)h * p.sm_h,
+                            p.l + (int64_t)b * p.sm_b + (int64_t)h * p.sm_h, p.S, p.NR, p.sa_s,
+                            p.sa_r, p.sm_s,
+                            (char*)p.out + ((int64_t)b * p.so_b + (int64_t)h * p.so_h) *
+                                               (p.out_f32 ? 4 : 2),
+                            p.out_f32, p.so_r, threadIdx.x);
 }
 
 // ------------------------------------------------------------- launch ----
 
 constexpr int NWAVES = 4;
 
-template <int KIND, bool ASYM, bool HAS_RES, bool SPARSE>
+template <int KIND, bool ASYM, bool HAS_RES, bool SPARSE, int ABL = 0>
 static hipError_t launch_t(const DecodeParams& a, hipStream_t stream) {
-    dim3 grid(a.num_splits * a.H, a.B);
-    hipLaunchKernelGGL((paged_decode_kernel<KIND, ASYM, HAS_RES, SPARSE, NWAVES>), grid,
-                       dim3(WAVE * NWAVES), 0, stream, a);
+    // Heads in pairs when the head count allows: both halves of every token
+    // row are then read together (the fp16 walk; INT8 keeps one head per
+    // group for its larger register footprint).
+    if constexpr (KIND == KV_FP16) {
+        if (a.H % 2 == 0) {
+        dim3 grid(a.num_splits * (a.H / 2), a.B);
+        hipLaunchKernelGGL((paged_decode_kernel<KIND, ASYM, HAS_RES, SPARSE, 2 * NWAVES, 2, ABL>),
+                           grid, dim3(WAVE * NWAVES * 2), 0, stream, a);
+        return hipGetLastError();
+        }
+    }
+    {
+        dim3 grid(a.num_splits * a.H, a.B);
+        hipLaunchKernelGGL((paged_decode_kernel<KIND, ASYM, HAS_RES, SPARSE, NWAVES, 1, ABL>),
+                           grid, dim3(WAVE * NWAVES), 0, stream, a);
+    }
     return hipGetLastError();
+}
+
+// LATENTSERVE_HIP_ABLATION (diagnostic only; the output is meaningless):
+//   loads        the fp16 dense walk with the arithmetic removed
+//   loads_noepi  ... and without the wave merge / partials / split merge
+//   noepi        the full arithmetic without the merge stages
+static int ablation() {
+    static const int v = [] {
+        const char* e = getenv("LATENTSERVE_HIP_ABLATION");
+        if (!e) return 0;
+        if (strcmp(e, "loads") == 0) return 1;
+        if (strcmp(e, "loads_noepi") == 0) return 2;
+        if (strcmp(e, "noepi") == 0) return 3;
+        return 0;
+    }();
+    return v;
 }
 
 static hipError_t launch_kernel(const DecodeParams& a, hipStream_t stream) {
     if (a.sel) return launch_t<KV_FP16, false, false, true>(a, stream);
+    if (a.kind == KV_FP16 && ablation() != 0) {
+        const int abl = ablation();
+        if (abl == 1) return launch_t<KV_FP16, false, false, false, 1>(a, stream);
+        if (abl == 2) return launch_t<KV_FP16, false, false, false, 2>(a, stream);
+        return launch_t<KV_FP16, false, false, false, 3>(a, stream);
+    }
     if (a.kind == KV_FP16) return launch_t<KV_FP16, false, false, false>(a, stream);
     const bool asym = a.k_zero != nullptr, res = a.k_res != nullptr;
     if (asym && res) return launch_t<KV_INT8, true, true, false>(a, stream);
@@ -634,16 +789,17 @@ hipError_t launch_decode(const DecodeParams& a_in, hipStream_t stream) {
     hipError_t e = launch_kernel(a, stream);
     if (e != hipSuccess || a.fuse || a.num_splits == 1) return e;
     CombineParams p;
-    p.acc = a.part_acc;
+    const int64_t rec = (int64_t)a.NR * HEAD_DIM + 2 * MAX_NREP;
+    p.acc = a.work;
     p.sa_r = HEAD_DIM;
-    p.sa_s = (int64_t)a.NR * HEAD_DIM;
-    p.sa_h = p.sa_s * a.num_splits;
+    p.sa_s = rec;
+    p.sa_h = rec * a.num_splits;
     p.sa_b = p.sa_h * a.H;
-    p.m = a.part_m;
-    p.l = a.part_l;
-    p.sm_s = a.NR;
-    p.sm_h = (int64_t)a.NR * a.num_splits;
-    p.sm_b = p.sm_h * a.H;
+    p.m = a.work + a.NR * HEAD_DIM;
+    p.l = p.m + MAX_NREP;
+    p.sm_s = rec;
+    p.sm_h = p.sa_h;
+    p.sm_b = p.sa_b;
     p.out = a.out;
     p.out_f32 = 0;
     p.so_b = a.so_b;
@@ -657,8 +813,7 @@ hipError_t launch_decode(const DecodeParams& a_in, hipStream_t stream) {
 }
 
 hipError_t launch_combine(const CombineParams& p, hipStream_t stream) {
-    // float4 partial loads when every row and split starts 16-byte aligned
-    const bool vec = ((uintptr_t)p.acc % 16 == 0) && p.sa_b % 4 == 0 && p.sa_h % 4 == 0 &&
+    const bool vec = (uintptr_t)p.acc % 16 == 0 && p.sa_b % 4 == 0 && p.sa_h % 4 == 0 &&
                      p.sa_s % 4 == 0 && p.sa_r % 4 == 0;
     if (vec)
         hipLaunchKernelGGL(combine_kernel<4>, dim3(p.B * p.H), dim3(256), 0, stream, p);

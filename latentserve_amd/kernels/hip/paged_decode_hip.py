@@ -25,11 +25,11 @@ from latentserve_amd.kernels.gqa import _scratch as scratch
 HEAD_DIM = 128
 PAGE = 16
 MAX_NREP = 16
-# Waves per workgroup in the decode kernel (each walks every NW-th page of
-# its split); must match NWAVES in csrc/ls_decode.hip.
+# Waves per (sequence, head, split) in the decode kernel (each walks every
+# NW-th page of its split); must match NWAVES in csrc/ls_decode.hip.
 WAVES_PER_GROUP = 4
 MAX_SPLITS = 1024
-GROUPS_PER_CU = 2
+WAVES_PER_CU = 8
 
 _CU_COUNT: dict = {}
 
@@ -45,14 +45,14 @@ def choose_splits(batch: int, kv_heads: int, num_pages: int,
                   device: Optional[torch.device] = None) -> int:
     """Splits per (sequence, KV head) for the MI355X kernel.
 
-    One resident wave of workgroups: GROUPS_PER_CU groups of four waves per
-    CU (the fp16 kernel's register budget allows two per CU), but never so
-    many splits that a wave gets fewer than two pages. Fixed by (batch,
-    heads, pages) alone, so a captured graph can pin it per context bucket.
+    One resident round of waves: every (sequence, head, split) is four
+    waves, and the fp16 kernel's register budget keeps WAVES_PER_CU of them
+    on a CU; never so many splits that a wave gets fewer than two pages.
+    Fixed by (batch, heads, pages) alone, so a captured graph can pin it per
+    context bucket.
     """
     cus = _cus(device) if device is not None and torch.cuda.is_available() else 256
-    target_groups = GROUPS_PER_CU * cus
-    by_cus = -(-target_groups // max(1, batch * kv_heads))
+    by_cus = -(-(WAVES_PER_CU * cus) // max(1, batch * kv_heads * WAVES_PER_GROUP))
     by_pages = max(1, num_pages // (2 * WAVES_PER_GROUP))
     return max(1, min(MAX_SPLITS, by_cus, by_pages))
 
@@ -118,16 +118,15 @@ def _aligned(t: torch.Tensor, nbytes: int) -> bool:
 
 
 def _buffers(tag: str, b: int, h: int, splits: int, n_rep: int, device):
-    """Persistent output and split scratch for one shape (graph-address stable)."""
+    """Persistent output, split workspace and arrival counters for one shape
+    (graph-address stable)."""
     out = scratch(f"{tag}_out", (b, h, MAX_NREP, HEAD_DIM), torch.float16, device)
+    cnt = scratch(f"{tag}_cnt", (2 * b * h,), torch.int32, device, init=0)
     if splits == 1:
-        return out, None, None, None, None
-    acc = scratch(f"{tag}_acc", (b, h, splits, n_rep, HEAD_DIM), torch.float32, device)
-    m = scratch(f"{tag}_m", (b, h, splits, n_rep), torch.float32, device)
-    l = scratch(f"{tag}_l", (b, h, splits, n_rep), torch.float32, device)
-    # Arrival counters: zero at rest, and every launch leaves them zero.
-    cnt = scratch(f"{tag}_cnt", (b * h,), torch.int32, device, init=0)
-    return out, acc, m, l, cnt
+        return out, None, cnt
+    nbytes = _lib.lib().ls_decode_workspace_bytes(b, h, n_rep, splits)
+    work = scratch(f"{tag}_work", (nbytes // 4,), torch.float32, device)
+    return out, work, cnt
 
 
 def _check_common(q, k_pool, v_pool, block_tables, seq_lens):
@@ -164,12 +163,11 @@ def paged_decode_hip(q, k_pool, v_pool, block_tables, seq_lens, max_seq_len: int
     splits = max(1, min(MAX_SPLITS, splits))
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
     is_int8 = k_pool.dtype == torch.int8
-    out, acc, m, l, cnt = _buffers("hip_i8" if is_int8 else "hip", b, h_kv, splits, n_rep,
-                                   q.device)
+    out, work, cnt = _buffers("hip_i8" if is_int8 else "hip", b, h_kv, splits, n_rep, q.device)
     L = _lib.lib()
     P, S = _lib.ptr, _lib.strides
-    common_tail = (P(out), S(out, 3), P(acc), P(m), P(l), P(cnt), b, h_kv, n_rep, d,
-                   k_pool.shape[1], splits, float(scale), _lib.stream_of(q.device))
+    common_tail = (P(out), S(out, 3), P(work), P(cnt), b, h_kv, n_rep, d, k_pool.shape[1],
+                   splits, int(max_seq_len), float(scale), _lib.stream_of(q.device))
     if is_int8:
         rc = L.ls_paged_decode_int8(
             P(q), S(q, 3), P(k_pool), P(v_pool), S(k_pool, 3), k_pool.shape[0],

@@ -64,13 +64,13 @@ def sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel,
     splits = num_splits or pdh.choose_splits(b, h, num_sel, q.device)
     splits = max(1, min(splits, max(1, num_sel), pdh.MAX_SPLITS))
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
-    out, acc, m, l, cnt = pdh._buffers("sparse", b, h, splits, n_rep, q.device)
+    out, work, cnt = pdh._buffers("sparse", b, h, splits, n_rep, q.device)
     P, S = _lib.ptr, _lib.strides
     rc = _lib.lib().ls_paged_sparse_fp16(
         P(q), S(q, 3), P(k_pool), P(v_pool), S(k_pool, 3), k_pool.shape[0],
         P(block_tables), block_tables.stride(0), block_tables.shape[1], P(seq_lens),
         P(sel), S(sel, 2), num_sel, 0.0 if ratio is None else float(ratio), int(recent),
-        P(out), S(out, 3), P(acc), P(m), P(l), P(cnt), b, h, n_rep, d, k_pool.shape[1],
-        splits, float(scale), _lib.stream_of(q.device))
+        P(out), S(out, 3), P(work), P(cnt), b, h, n_rep, d, k_pool.shape[1],
+        splits, 0, float(scale), _lib.stream_of(q.device))
     _lib.check(rc, "ls_paged_sparse_fp16")
     return out[:, :, :n_rep]

@@ -39,7 +39,12 @@ def test_python_binding_covers_the_header():
 
 
 def test_abi_version(lib):
-    assert lib.ls_abi_version() == 1
+    assert lib.ls_abi_version() == 2
+
+
+def test_workspace_size(lib):
+    assert lib.ls_decode_workspace_bytes(16, 2, 6, 1) == 0
+    assert lib.ls_decode_workspace_bytes(16, 2, 6, 8) == 16 * 2 * 8 * (6 * 128 + 32) * 4
 
 
 def _strides(*v):
@@ -49,14 +54,14 @@ def _strides(*v):
 def _call_fp16(lib, **over):
     args = dict(q=1024, qs=_strides(1536, 768, 128), k=4096, v=8192,
                 kvs=_strides(4096, 256, 128), nb=10, bt=16, bts=4, mp=4, sl=32, out=64,
-                outs=_strides(1536, 768, 128), pa=None, pm=None, pl=None, cnt=None,
-                B=2, H=2, NR=6, D=128, P=16, S=1, scale=0.088)
+                outs=_strides(1536, 768, 128), work=None, cnt=64,
+                B=2, H=2, NR=6, D=128, P=16, S=1, msl=0, scale=0.088)
     args.update(over)
     a = args
     return lib.ls_paged_decode_fp16(a["q"], a["qs"], a["k"], a["v"], a["kvs"], a["nb"], a["bt"],
-                                    a["bts"], a["mp"], a["sl"], a["out"], a["outs"], a["pa"],
-                                    a["pm"], a["pl"], a["cnt"], a["B"], a["H"], a["NR"], a["D"],
-                                    a["P"], a["S"], a["scale"], None)
+                                    a["bts"], a["mp"], a["sl"], a["out"], a["outs"], a["work"],
+                                    a["cnt"], a["B"], a["H"], a["NR"], a["D"], a["P"], a["S"],
+                                    a["msl"], a["scale"], None)
 
 
 @pytest.mark.parametrize("over,needle", [
@@ -65,7 +70,9 @@ def _call_fp16(lib, **over):
     (dict(NR=17), "n_rep"),
     (dict(q=None), "null"),
     (dict(q=1026), "aligned"),
-    (dict(S=4), "num_splits > 1 needs"),
+    (dict(cnt=None), "counters is required"),
+    (dict(S=4, cnt=64), "num_splits > 1 needs"),
+    (dict(S=4, work=4096 + 64, cnt=64), "256-byte"),
     (dict(kvs=_strides(4096, 256, 127)), "aligned"),
 ])
 def test_bad_arguments_are_rejected_before_launch(lib, over, needle):

@@ -44,7 +44,7 @@ def run_fp16(case, num_splits=None, max_len=None):
 
 def test_library_is_the_hip_build():
     from latentserve_amd import _lib
-    assert _lib.lib().ls_abi_version() == 1
+    assert _lib.lib().ls_abi_version() == 2
 
 
 @pytest.mark.parametrize("splits", [None, 1, 3, 64])
@@ -278,3 +278,15 @@ def test_sparse_full_selection_is_dense():
     # A budgeted call over an unsorted list attends exactly the first n entries.
     got = ps.sparse_decode(Q, K, V, T, L, REV, ratio=1.0).float().cpu().numpy()
     assert_close(got, oracle.sparse_decode(q, k, v, t, l, rev, ratio=1.0), ATOL, RTOL, "budget")
+
+
+@pytest.mark.parametrize("max_len", [1, 700, 3000, 1 << 20])
+def test_any_max_seq_len_gives_the_same_result(max_len):
+    """max_seq_len only sets the partition of pages over splits: too small a
+    bound is re-derived on the device per sequence, too large wastes splits;
+    the output never changes."""
+    case = paged_case([2900, 700, 33, 1], seed=21)
+    want = dense_attention(*case)
+    for splits in (1, 5, 16):
+        assert_close(run_fp16(case, splits, max_len=max_len), want, ATOL, RTOL,
+                     f"max_len={max_len} splits={splits}")
