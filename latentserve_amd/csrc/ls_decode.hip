@@ -58,14 +58,14 @@ struct DecodeSmem {
     // per head, the block and page of every list entry (page-subset walk).
     // Rows of the wave states are padded by 16 bytes so that the 16 rows a
     // wave writes at once fall in different banks.
+    // The table has its own space so that a wave can store its state the
+    // moment its walk ends, while the others still resolve items.
     static constexpr int ROW = HEAD_DIM + 4;
-    static constexpr int ENT_INTS = NWT * MAX_NREP * ROW;
-    float m[NWT][MAX_NREP];
-    float l[NWT][MAX_NREP];
-    union {
-        int ent[ENT_INTS];
-        float acc[NWT][MAX_NREP][ROW];            // after it: one head's wave states
-    };
+    static constexpr int ENT_INTS = 2048 * HG;
+    float m[HG][NWT][MAX_NREP];
+    float l[HG][NWT][MAX_NREP];
+    float acc[HG][NWT][MAX_NREP][ROW];
+    int ent[ENT_INTS];
     int is_last[HG];
     int claim;
 };
@@ -390,6 +390,15 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     const int spec_lo = host_split ? split * a.pages_per_split : 0;
     if (host_split && (int)threadIdx.x < a.pages_per_split && spec_lo + (int)threadIdx.x < a.max_pages)
         spec_blk = a.block_tables[(int64_t)b * a.sbt_b + spec_lo + threadIdx.x];
+    // ... and lane u < NB of each wave fetches the block of the wave's own
+    // fixed item u, so its first page loads need neither the table nor the
+    // barrier.
+    int first_blk = -1;
+    if (host_split && lane < NB) {
+        const int e = (wv + lane * NWT) / HG;
+        if (e < a.pages_per_split && spec_lo + e < a.max_pages)
+            first_blk = a.block_tables[(int64_t)b * a.sbt_b + spec_lo + e];
+    }
 
     const int len = a.seq_lens[b];
     int num_pages = (len + PAGE - 1) / PAGE;
@@ -443,7 +452,8 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             if (HAS_RES && pg == num_pages - 1 && !res_ok) blk = -1;
         }
     };
-    if (cached) {
+    auto fill_table = [&]() {
+        if (!cached) return;
         if (SPARSE) {
             for (int i = threadIdx.x; i < n_ent * HG; i += WAVE * NWT) {
                 const int hh = i / n_ent, e = i % n_ent;
@@ -467,7 +477,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 sm.ent[e] = blk;
             }
         }
-    }
+    };
 
     // Query operands of the group's heads: row c (zero beyond n_rep),
     // channels 32j+8g..+8.
@@ -502,7 +512,6 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         st[hh].l = 0.f;
         st[hh].z = 0.f;
     }
-    __syncthreads();
 
     // Item i: entry i / HG of head i % HG (the heads of a page are adjacent
     // items, so a page's token rows are requested whole at about one time).
@@ -523,6 +532,19 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             pg = lo + e;
         }
     };
+    // The wave's fixed item u (dense walk with the host's split): its block
+    // is in lane u of first_blk.
+    auto resolve_first = [&](int u, int i, int& blk, int& pg, int& hh) {
+        hh = HG == 1 ? 0 : i % HG;
+        const int e = HG == 1 ? i : i / HG;
+        pg = lo + e;
+        blk = __builtin_amdgcn_readlane(first_blk, u);
+        if (i >= n_items || !(pg >= 0 && pg < num_pages) || blk < 0 || blk >= a.num_blocks ||
+            (HAS_RES && pg == num_pages - 1 && !res_ok)) {
+            blk = -1;
+            pg = -1;
+        }
+    };
     auto resolve_mem = [&](int i, int& blk, int& pg, int& hh) {
         hh = HG == 1 ? 0 : i % HG;
         const int e = HG == 1 ? i : i / HG;
@@ -539,18 +561,30 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     auto walk = [&](auto resolve) {
         PageBuf buf[NB];
         int item[NB], pgs[NB], ok[NB], hds[NB];
-        auto issue = [&](int slot, int it) {
+        auto issue_with = [&](auto res, int slot, int it) {
             int blk, pg, hh;
             item[slot] = it;
-            resolve(it, blk, pg, hh);
+            res(it, blk, pg, hh);
             ok[slot] = blk >= 0;
             pgs[slot] = pg;
             hds[slot] = hh;
             load_page<KIND, ASYM, HAS_RES>(a, buf[slot], ok[slot] ? blk : 0, ok[slot] ? pg : -1,
                                            num_pages, b, h0 + hh, g, c);
         };
+        auto issue = [&](int slot, int it) { issue_with(resolve, slot, it); };
+        // The first items are fixed (wave wv takes wv, wv + NWT, ...): their
+        // blocks come straight from the table, so their loads are in flight
+        // while the group fills the item table and meets at the barrier.
 #pragma unroll
-        for (int u = 0; u < PF_DEPTH; ++u) issue(u, wv + u * NWT);
+        for (int u = 0; u < PF_DEPTH; ++u) {
+            if (spec_ok)
+                issue_with([&](int i, int& blk, int& pg, int& hh) { resolve_first(u, i, blk, pg, hh); },
+                           u, wv + u * NWT);
+            else
+                issue_with(resolve_mem, u, wv + u * NWT);
+        }
+        fill_table();
+        __syncthreads();
         int it_n = wv + PF_DEPTH * NWT;
         if (item[0] >= n_items) return;
         while (true) {
@@ -601,67 +635,74 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         return;
     }
 
-    // ---- merge the waves' states in LDS, one head at a time ----
+    // ---- merge the waves' states in LDS (all heads at once); each wave
+    // stores its state as soon as its walk ends ----
     // One record per (b, h, split): acc[NR][128], m[16], l[16].  Every cache
     // line of a record is written by this group alone.
     const int64_t rec = (int64_t)NR * HEAD_DIM + 2 * MAX_NREP;
+    float lrow[HG];
 #pragma unroll
     for (int hh = 0; hh < HG; ++hh) {
-        const float lrow = group4_sum(st[hh].l);
+        lrow[hh] = group4_sum(st[hh].l);
         if (ASYM) {
             const float zrow = group4_sum(st[hh].z);
 #pragma unroll
             for (int t = 0; t < 8; ++t) st[hh].acc[t] += zrow;
         }
-        __syncthreads();                 // the table (or the previous head) is dead
-        if (g == 0) {
-            sm.m[wv][c] = st[hh].m;
-            sm.l[wv][c] = lrow;
-        }
-        // the lane's 32 channels 32g..32g+31 (channel 32g + 8i + t is element
-        // i of tile t) as eight 16-byte stores
+    }
+    if (c < NR) {                        // rows past n_rep hold nothing
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            f4 v;
+        for (int hh = 0; hh < HG; ++hh) {
+            if (g == 0) {
+                sm.m[hh][wv][c] = st[hh].m;
+                sm.l[hh][wv][c] = lrow[hh];
+            }
+            // the lane's 32 channels 32g..32g+31 (channel 32g + 8i + t is
+            // element i of tile t) as eight 16-byte stores
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = st[hh].acc[4 * (j % 2) + e][j / 2];
-            *(f4*)&sm.acc[wv][c][32 * g + 4 * j] = v;
+            for (int j = 0; j < 8; ++j) {
+                f4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = st[hh].acc[4 * (j % 2) + e][j / 2];
+                *(f4*)&sm.acc[hh][wv][c][32 * g + 4 * j] = v;
+            }
         }
-        __syncthreads();
+    }
+    __syncthreads();
 
+    for (int idx = threadIdx.x; idx < HG * NR * HEAD_DIM; idx += WAVE * NWT) {
+        const int hh = idx / (NR * HEAD_DIM), ri = idx % (NR * HEAD_DIM);
+        const int r = ri / HEAD_DIM, d = ri % HEAD_DIM;
+        float mg = neg_inf();
+#pragma unroll
+        for (int u = 0; u < NWT; ++u) mg = fmaxf(mg, sm.m[hh][u][r]);
+        float lt = 0.f, at = 0.f;
+#pragma unroll
+        for (int u = 0; u < NWT; ++u) {
+            const float wt = mg == neg_inf() ? 0.f : fast_exp2(sm.m[hh][u][r] - mg);
+            lt += sm.l[hh][u][r] * wt;
+            at += sm.acc[hh][u][r][d] * wt;
+        }
         const int64_t bh = (int64_t)b * H + h0 + hh;
         float* pacc = a.work + (bh * S + split) * rec;
         float* pm = pacc + NR * HEAD_DIM;
         float* pl = pm + MAX_NREP;
-        for (int idx = threadIdx.x; idx < NR * HEAD_DIM; idx += WAVE * NWT) {
-            const int r = idx / HEAD_DIM, d = idx % HEAD_DIM;
-            float mg = neg_inf();
-#pragma unroll
-            for (int u = 0; u < NWT; ++u) mg = fmaxf(mg, sm.m[u][r]);
-            float lt = 0.f, at = 0.f;
-#pragma unroll
-            for (int u = 0; u < NWT; ++u) {
-                const float wt = mg == neg_inf() ? 0.f : fast_exp2(sm.m[u][r] - mg);
-                lt += sm.l[u][r] * wt;
-                at += sm.acc[u][r][d] * wt;
+        if (single) {
+            a.out[(int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h + (int64_t)r * a.so_r + d] =
+                (half_t)(at / fmaxf(lt, 1e-20f));
+        } else if (a.fuse) {
+            // Device-coherent (write-through) stores: the group that merges
+            // may run on another XCD, whose L2 does not see this one's.
+            store_coherent(pacc + ri, at);
+            if (d == 0) {
+                store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
+                store_coherent(pl + r, lt);
             }
-            if (single) {
-                a.out[(int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h + (int64_t)r * a.so_r + d] =
-                    (half_t)(at / fmaxf(lt, 1e-20f));
-            } else if (a.fuse) {
-                // Device-coherent (write-through) stores: the group that merges
-                // may run on another XCD, whose L2 does not see this one's.
-                store_coherent(pacc + idx, at);
-                if (d == 0) {
-                    store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
-                    store_coherent(pl + r, lt);
-                }
-            } else {
-                pacc[idx] = at;
-                if (d == 0) {
-                    pm[r] = mg * LN2;
-                    pl[r] = lt;
-                }
+        } else {
+            pacc[ri] = at;
+            if (d == 0) {
+                pm[r] = mg * LN2;
+                pl[r] = lt;
             }
         }
     }
