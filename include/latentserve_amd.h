@@ -24,10 +24,11 @@
  *   workspace   fp32 scratch of ls_decode_workspace_bytes() bytes, 256-byte
  *               aligned (one record per (b, h, split): acc[n_rep][128],
  *               m[16], l[16]); needed only when num_splits > 1
- *   counters    int32 [2 * B * H_kv], zero before the first call; every
- *               call leaves it zero again (per (sequence, head): an arrival
- *               count of split groups and a page-claim count).  Calls that
- *               share scratch must be ordered on one stream.
+ *   counters    int32 [B * H_kv] (larger is fine), zero before the first
+ *               call; every call leaves it zero again (per (sequence, head):
+ *               the count of split workgroups that have stored their
+ *               partials).  Calls that share scratch must be ordered on one
+ *               stream.
  *   max_seq_len the longest sequence in the call (the caller's bound, e.g.
  *               a graph bucket); it sets the pages per split.  A sequence
  *               longer than it is still handled (its split is re-derived on
@@ -69,11 +70,10 @@ size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_spl
  * paged_decode_cuda() for an fp16 pool (kernels/cuda/paged_decode_cuda.py:202-252,
  * kernels/cuda/paged_decode_fp16.cu:55-64) behind paged_decode_attention
  * (kernels/gqa/paged_decode.py:709-829).  One launch: the splits are merged
- * by the last workgroup of each (sequence, head) to finish.  Pages are
- * claimed dynamically by every wave of every split of a (sequence, head),
- * so the splits only set how many groups share the walk.  With
- * num_splits == 1 the output is written directly and workspace is not
- * touched (it may be NULL). */
+ * by the last workgroup of each (sequence, head) to finish.  Each split is a
+ * contiguous page range whose pages the waves of its workgroup claim one by
+ * one.  With num_splits == 1 the output is written directly and workspace is
+ * not touched (it may be NULL). */
 int ls_paged_decode_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
                          const void* v_pool, const int64_t* kv_strides, int num_blocks,
                          const int32_t* block_tables, int64_t bt_stride, int max_pages,
