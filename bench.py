@@ -9,7 +9,8 @@ MALL can serve a layer's 268 MB from cache; 28 calls are captured in one HIP
 graph and the graph is replayed, timed with HIP events on the launch stream.
 
 Configs: c1 B1x2048, c2 B16x16384 (the headline), c3
-B8x32768, c3r ragged B16 with lengths ~U[512, 32768], c4 INT8 B16x16384.
+B8x32768, c3r ragged B16 with lengths ~U[512, 32768], c4 INT8 B16x16384,
+c5 sparse (50% of pages, selected on the GPU each step) B8x32768.
 Inputs are synthetic N(0,1) fp16 from a seeded device generator; block
 tables are a seeded permutation of the pool (non-contiguous pages).
 
@@ -43,6 +44,9 @@ CONFIGS = {
     "flat": dict(batch=512, ctx=512, kind="fp16", workload="fp16 paged decode B512 x 512"),
     "c4": dict(batch=16, ctx=16384, kind="int8",
                workload="INT8 paged decode B16 x 16384 (fp32 scales, fp16 last-page K residual)"),
+    "c5": dict(batch=8, ctx=32768, kind="sparse", ratio=0.5,
+               workload="sparse 50% paged decode B8 x 32768 (page index + top-k + page-subset "
+                        "attention)"),
 }
 
 
@@ -81,6 +85,18 @@ def algorithmic_bytes(cfg, lens) -> int:
     pages = [(int(l) + PAGE - 1) // PAGE for l in lens]
     tokens = sum(p * PAGE for p in pages)          # whole pages are read
     b = len(lens)
+    if cfg["kind"] == "sparse":
+        # indexer: kmin + kmax of every scored page; attention: the kept pages
+        ratio = cfg["ratio"]
+        width = (cfg["ctx"] + PAGE - 1) // PAGE
+        k = min(width, max(3, math.ceil(ratio * width)))
+        scored = sum(max(0, p - 3) for p in pages)
+        kept = sum(min(k, p, max(3, math.ceil(ratio * p))) for p in pages)
+        bounds = scored * H_KV * D * 2 * 2
+        kv = kept * PAGE * H_KV * D * 2 * 2
+        q = b * H_KV * N_REP * D * 2
+        sel = b * H_KV * k * 4
+        return bounds + kv + 2 * q + sum(pages) * 4 + kept * H_KV * 4 + sel + b * 4
     if cfg["kind"] == "fp16":
         kv = tokens * H_KV * D * 2 * 2
     else:
@@ -119,6 +135,12 @@ def build_workload(cfg, layers, seed=0, contiguous=False):
         v = torch.randn(nb, PAGE, H_KV, D, device=dev, generator=g, dtype=torch.float16)
         if cfg["kind"] == "int8":
             pools.append((q,) + quantize_layer(k, v, tables, seq))
+        elif cfg["kind"] == "sparse":
+            from latentserve_amd.kernels.hip import paged_sparse as ps
+            kmin = torch.empty(nb, H_KV, D, dtype=torch.float16, device=dev)
+            kmax = torch.empty_like(kmin)
+            ps.rebuild_bounds(k, kmin, kmax)
+            pools.append((q, k, v, kmin, kmax))
         else:
             pools.append((q, k, v))
     return tables, seq, pools, int(max_pages * PAGE)
@@ -154,6 +176,11 @@ def make_call(cfg, tables, seq, layer, max_len, splits):
         q, kq, vq, ks, vs, res, rr = layer
         return lambda: pdh.paged_decode_hip(q, kq, vq, tables, seq, max_len, num_splits=splits,
                                             k_scale=ks, v_scale=vs, k_residual=res, res_rows=rr)
+    if cfg["kind"] == "sparse":
+        from latentserve_amd.kernels.hip import paged_sparse as ps
+        q, k, v, kmin, kmax = layer
+        return lambda: ps.sparse_attention(q, k, v, tables, seq, kmin, kmax, ratio=cfg["ratio"],
+                                           max_seq_len=max_len)
     q, k, v = layer
     return lambda: pdh.paged_decode_hip(q, k, v, tables, seq, max_len, num_splits=splits)
 
@@ -171,6 +198,19 @@ def cpu_baseline(cfg, tables, seq, layer, n_seqs):
     n = min(b, n_seqs or b)
     lens = seq.cpu().numpy()[:n]
     t = tables.cpu().numpy()[:n]
+    if cfg["kind"] == "sparse":
+        q, k, v, kmin, kmax = [x.cpu().numpy() for x in layer]
+        width = t.shape[1]
+        kk = oracle.budget(cfg["ratio"], width)
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            scores = oracle.page_scores(q[:n], kmin, kmax, t, lens)
+            sel = oracle.select(scores, kk)
+            oracle.sparse_decode(q[:n], k, v, t, lens, sel, ratio=cfg["ratio"])
+            times.append(time.perf_counter() - t0)
+        return _cpu_result(cfg, lens, b, n, sorted(times)[1], threads,
+                           "C oracle page_scores + stable top-k + sparse_decode")
     if cfg["kind"] == "int8":
         q, kq, vq, ks, vs, res, rr = [x.cpu().numpy() for x in layer]
         args = (q[:n], kq, vq, t, lens)
@@ -184,7 +224,11 @@ def cpu_baseline(cfg, tables, seq, layer, n_seqs):
         t0 = time.perf_counter()
         oracle.paged_decode(*args, num_splits=1, **extra)
         times.append(time.perf_counter() - t0)
-    dt = sorted(times)[1]                                   # median of 3
+    return _cpu_result(cfg, lens, b, n, sorted(times)[1], threads,
+                       "C oracle paged_decode (num_splits=1)")
+
+
+def _cpu_result(cfg, lens, b, n, dt, threads, what):
     sample_bytes = algorithmic_bytes(cfg, lens)
     return {
         "value": round(sample_bytes / dt / 1e9, 3),
@@ -192,7 +236,7 @@ def cpu_baseline(cfg, tables, seq, layer, n_seqs):
         "cores": threads,
         "kind": "port",
         "sample": f"{n} of {b} sequences of one layer-step ({sample_bytes / 1e6:.1f} MB), "
-                  f"C oracle (oracle/ls_oracle.c, OpenMP) with num_splits=1, median of 3: "
+                  f"{what} (oracle/ls_oracle.c, OpenMP), median of 3: "
                   f"{dt * 1e3:.1f} ms -> {dt * 1e3 * b / n:.1f} ms per full layer-step",
         "ms_per_layer_step": round(dt * 1e3 * b / n, 3),
     }
@@ -276,7 +320,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16" if cfg["kind"] == "fp16" else "int8 KV / fp16 q",
+        "dtype": "int8 KV / fp16 q" if cfg["kind"] == "int8" else "fp16",
         "data": "synthetic N(0,1), seeded device generator, permuted block tables",
         "config": {"workload": cfg["workload"], "batch": cfg["batch"], "ctx": cfg["ctx"],
                    "kv_heads": H_KV, "n_rep": N_REP, "head_dim": D, "page": PAGE,

@@ -125,6 +125,65 @@ int ls_combine_splits(const float* part_acc, const int64_t* acc_strides, const f
                       const int64_t* out_strides, int batch, int kv_heads, int num_splits,
                       int n_rep, int head_dim, void* stream);
 
+/* ---- page selection for sparse decode -------------------------------- *
+ * kmin / kmax  [num_blocks, H_kv, 128] fp16, per-page per-channel min / max
+ *              of K; bound_strides[2] = (block, head)
+ * scores       [B, H_kv, >= max_pages] fp32; score_strides[2] = (b, h)
+ * sel          [B, H_kv, >= k] int32 page indices; sel_strides[2] = (b, h)
+ */
+
+/* Quest page scores: for page p < pages(b) of each (sequence, KV head), the
+ * max over its n_rep query heads of sum_d max(q_d*kmin_d, q_d*kmax_d); page 0
+ * and the last `recent` pages +inf, pages past the sequence (or whose block
+ * id lies outside the pool) -inf.  Replaces page_index
+ * (kernels/cuda/paged_sparse_fp16.cu:78-130) / page_scores
+ * (kernels/cuda/paged_sparse.py:104-123). */
+int ls_page_scores(const void* q, const int64_t* q_strides, const void* kmin, const void* kmax,
+                   const int64_t* bound_strides, int num_blocks, const int32_t* block_tables,
+                   int64_t bt_stride, int max_pages, const int32_t* seq_lens, float* scores,
+                   const int64_t* score_strides, int batch, int kv_heads, int n_rep, int head_dim,
+                   int page, int recent, void* stream);
+
+/* Top-k pages per (sequence, KV head) from scores [.., 0:num_pages].
+ * Replaces select (kernels/cuda/paged_sparse.py:164-168, torch.topk).
+ * Order of equal scores: lower page first.  sorted = 1: sel[0:k] best
+ * first.  sorted = 0: with ratio > 0, sel[0:n_b] holds the n_b =
+ * min(max(recent+1, ceilf(ratio*pages_b)), pages_b, k) best pages of
+ * sequence b (the entries ls_paged_sparse_fp16 attends with that ratio) and
+ * sel[n_b:k] the next ones, each part in page order; ratio <= 0: the k best in
+ * page order.  k <= num_pages <= 8192. */
+int ls_page_select(const float* scores, const int64_t* score_strides, const int32_t* seq_lens,
+                   int batch, int kv_heads, int num_pages, int k, float ratio, int recent,
+                   int sorted, int32_t* sel, const int64_t* sel_strides, void* stream);
+
+/* ls_page_scores + ls_page_select (sorted = 0) in one launch: the index and
+ * select steps of sparse_attention (kernels/cuda/paged_sparse.py:222-251).
+ * counters int32 [B * H_kv], zero before the first call and left zero.
+ * scores and its (b, h) strides must be 128-byte aligned (each group of 32
+ * pages owns one line); k <= max_pages <= 8192.  With sel == NULL this is
+ * ls_page_scores. */
+int ls_sparse_index(const void* q, const int64_t* q_strides, const void* kmin, const void* kmax,
+                    const int64_t* bound_strides, int num_blocks, const int32_t* block_tables,
+                    int64_t bt_stride, int max_pages, const int32_t* seq_lens, float* scores,
+                    const int64_t* score_strides, int32_t* counters, int k, float ratio,
+                    int recent, int32_t* sel, const int64_t* sel_strides, int batch, int kv_heads,
+                    int n_rep, int head_dim, int page, void* stream);
+
+/* Page bounds on write: k_new [B, H_kv, 128] fp16 (kn_strides[2] = (b, h))
+ * was just written at flat slot slots[b] (int64); a page's first token
+ * resets its bounds, later tokens widen them.  Slots outside the pool are
+ * skipped.  Replaces page_bounds_update (paged_sparse_fp16.cu:54-72) /
+ * update_bounds (kernels/cuda/paged_sparse.py:86-101). */
+int ls_page_bounds_update(const void* k_new, const int64_t* kn_strides, const int64_t* slots,
+                          void* kmin, void* kmax, const int64_t* bound_strides, int num_blocks,
+                          int batch, int kv_heads, int head_dim, int page, void* stream);
+
+/* Every block's bounds over all 16 rows of the K pool (kv_strides as for
+ * the decode calls).  Replaces rebuild_bounds (kernels/cuda/paged_sparse.py:81-84). */
+int ls_page_bounds_rebuild(const void* k_pool, const int64_t* kv_strides, int num_blocks,
+                           void* kmin, void* kmax, const int64_t* bound_strides, int kv_heads,
+                           int head_dim, int page, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

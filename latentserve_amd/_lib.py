@@ -41,6 +41,18 @@ _SIGNATURES = {
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
         _I32, _F32, _I32, _VP, _I64P, _VP, _VP,
         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
+    "ls_page_scores": [
+        _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
+        _I32, _I32, _I32, _I32, _I32, _I32, _VP],
+    "ls_sparse_index": [
+        _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
+        _VP, _I32, _F32, _I32, _VP, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
+    "ls_page_select": [
+        _VP, _I64P, _VP, _I32, _I32, _I32, _I32, _F32, _I32, _I32, _VP, _I64P, _VP],
+    "ls_page_bounds_update": [
+        _VP, _I64P, _VP, _VP, _VP, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
+    "ls_page_bounds_rebuild": [
+        _VP, _I64P, _I32, _VP, _VP, _I64P, _I32, _I32, _I32, _VP],
     "ls_combine_splits": [
         _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
 }

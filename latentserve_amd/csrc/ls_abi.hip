@@ -16,6 +16,7 @@
 #include "../../include/latentserve_amd.h"
 #include "ls_common.h"
 #include "ls_decode.h"
+#include "ls_sparse.h"
 
 namespace {
 
@@ -126,7 +127,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 2; }
+int ls_abi_version(void) { return 3; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -275,6 +276,173 @@ int ls_combine_splits(const float* part_acc, const int64_t* acc_strides, const f
     p.S = num_splits;
     p.NR = n_rep;
     return hip_status(ls::launch_combine(p, (hipStream_t)stream), "ls_combine_splits");
+}
+
+int ls_page_scores(const void* q, const int64_t* q_strides, const void* kmin, const void* kmax,
+                   const int64_t* bound_strides, int num_blocks, const int32_t* block_tables,
+                   int64_t bt_stride, int max_pages, const int32_t* seq_lens, float* scores,
+                   const int64_t* score_strides, int batch, int kv_heads, int n_rep, int head_dim,
+                   int page, int recent, void* stream) {
+    return ls_sparse_index(q, q_strides, kmin, kmax, bound_strides, num_blocks, block_tables,
+                           bt_stride, max_pages, seq_lens, scores, score_strides, nullptr, 0,
+                           0.f, recent, nullptr, nullptr, batch, kv_heads, n_rep, head_dim, page,
+                           stream);
+}
+
+int ls_sparse_index(const void* q, const int64_t* q_strides, const void* kmin, const void* kmax,
+                    const int64_t* bound_strides, int num_blocks, const int32_t* block_tables,
+                    int64_t bt_stride, int max_pages, const int32_t* seq_lens, float* scores,
+                    const int64_t* score_strides, int32_t* counters, int k, float ratio,
+                    int recent, int32_t* sel, const int64_t* sel_strides, int batch, int kv_heads,
+                    int n_rep, int head_dim, int page, void* stream) {
+    if (!q || !q_strides || !kmin || !kmax || !bound_strides || !block_tables || !seq_lens ||
+        !scores || !score_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim != ls::HEAD_DIM) return fail(LS_ERR_INVALID, "head_dim must be 128, got %d", head_dim);
+    if (page != ls::PAGE) return fail(LS_ERR_INVALID, "page (block_size) must be 16, got %d", page);
+    if (n_rep < 1 || n_rep > ls::MAX_NREP)
+        return fail(LS_ERR_INVALID, "n_rep must be in [1, %d], got %d", ls::MAX_NREP, n_rep);
+    if (batch < 0 || batch > 65535 || kv_heads < 1 || kv_heads > 65535)
+        return fail(LS_ERR_INVALID, "bad batch (%d) or kv_heads (%d)", batch, kv_heads);
+    if (num_blocks < 0 || max_pages < 0 || recent < 0)
+        return fail(LS_ERR_INVALID, "bad num_blocks, max_pages or recent");
+    if (!rows_aligned(q, q_strides, 3, 2, 16))
+        return fail(LS_ERR_INVALID, "q rows must be 16-byte aligned");
+    if (!rows_aligned(kmin, bound_strides, 2, 2, 16) || !rows_aligned(kmax, bound_strides, 2, 2, 16))
+        return fail(LS_ERR_INVALID, "kmin/kmax rows must be 16-byte aligned");
+    if (!aligned(scores, 4)) return fail(LS_ERR_INVALID, "scores must be 4-byte aligned");
+    const bool fused = sel != nullptr;
+    if (fused) {
+        if (!sel_strides || !counters)
+            return fail(LS_ERR_INVALID, "selection needs sel_strides and counters");
+        if (k < 1 || k > max_pages)
+            return fail(LS_ERR_INVALID, "k must be in [1, max_pages=%d], got %d", max_pages, k);
+        if (max_pages > ls::SELECT_MAX_PAGES)
+            return fail(LS_ERR_INVALID, "selection supports max_pages <= %d, got %d",
+                        ls::SELECT_MAX_PAGES, max_pages);
+        // each index group's 32 scores must own one 128-byte line
+        if (!rows_aligned(scores, score_strides, 2, 4, 128))
+            return fail(LS_ERR_INVALID,
+                        "with selection, scores and its (b, h) strides must be 128-byte aligned");
+    }
+    if (batch == 0 || max_pages == 0) return LS_OK;
+    ls::IndexParams a;
+    a.q = q;
+    a.sq_b = q_strides[0];
+    a.sq_h = q_strides[1];
+    a.sq_r = q_strides[2];
+    a.kmin = kmin;
+    a.kmax = kmax;
+    a.sb_b = bound_strides[0];
+    a.sb_h = bound_strides[1];
+    a.num_blocks = num_blocks;
+    a.block_tables = block_tables;
+    a.sbt_b = bt_stride;
+    a.max_pages = max_pages;
+    a.seq_lens = seq_lens;
+    a.scores = scores;
+    a.ss_b = score_strides[0];
+    a.ss_h = score_strides[1];
+    a.B = batch;
+    a.H = kv_heads;
+    a.NR = n_rep;
+    a.recent = recent;
+    a.sel = sel;
+    a.sl_b = fused ? sel_strides[0] : 0;
+    a.sl_h = fused ? sel_strides[1] : 0;
+    a.k = k;
+    a.ratio = ratio;
+    a.counters = counters;
+    return hip_status(ls::launch_page_index(a, (hipStream_t)stream),
+                      fused ? "ls_sparse_index" : "ls_page_scores");
+}
+
+int ls_page_select(const float* scores, const int64_t* score_strides, const int32_t* seq_lens,
+                   int batch, int kv_heads, int num_pages, int k, float ratio, int recent,
+                   int sorted, int32_t* sel, const int64_t* sel_strides, void* stream) {
+    if (!scores || !score_strides || !sel || !sel_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (ratio > 0.f && !seq_lens) return fail(LS_ERR_INVALID, "a ratio needs seq_lens");
+    if (batch < 0 || batch > 65535 || kv_heads < 1 || kv_heads > 65535 || recent < 0)
+        return fail(LS_ERR_INVALID, "bad batch, kv_heads or recent");
+    if (num_pages < 0 || num_pages > ls::SELECT_MAX_PAGES)
+        return fail(LS_ERR_INVALID, "num_pages must be in [0, %d], got %d", ls::SELECT_MAX_PAGES,
+                    num_pages);
+    if (k < 0 || k > num_pages)
+        return fail(LS_ERR_INVALID, "k must be in [0, num_pages=%d], got %d", num_pages, k);
+    if (batch == 0 || k == 0) return LS_OK;
+    ls::SelectParams a;
+    a.scores = scores;
+    a.ss_b = score_strides[0];
+    a.ss_h = score_strides[1];
+    a.seq_lens = seq_lens;
+    a.B = batch;
+    a.H = kv_heads;
+    a.P = num_pages;
+    a.k = k;
+    a.recent = recent;
+    a.sorted = sorted ? 1 : 0;
+    a.ratio = sorted ? 0.f : ratio;
+    a.sel = sel;
+    a.sl_b = sel_strides[0];
+    a.sl_h = sel_strides[1];
+    return hip_status(ls::launch_page_select(a, (hipStream_t)stream), "ls_page_select");
+}
+
+int ls_page_bounds_update(const void* k_new, const int64_t* kn_strides, const int64_t* slots,
+                          void* kmin, void* kmax, const int64_t* bound_strides, int num_blocks,
+                          int batch, int kv_heads, int head_dim, int page, void* stream) {
+    if (!k_new || !kn_strides || !slots || !kmin || !kmax || !bound_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim != ls::HEAD_DIM) return fail(LS_ERR_INVALID, "head_dim must be 128, got %d", head_dim);
+    if (page != ls::PAGE) return fail(LS_ERR_INVALID, "page (block_size) must be 16, got %d", page);
+    if (batch < 0 || batch > (1 << 30) || kv_heads < 1 || kv_heads > 65535 || num_blocks < 0)
+        return fail(LS_ERR_INVALID, "bad batch, kv_heads or num_blocks");
+    if (!rows_aligned(k_new, kn_strides, 2, 2, 4) || !rows_aligned(kmin, bound_strides, 2, 2, 4) ||
+        !rows_aligned(kmax, bound_strides, 2, 2, 4))
+        return fail(LS_ERR_INVALID, "k_new, kmin and kmax rows must be 4-byte aligned");
+    if (batch == 0) return LS_OK;
+    ls::BoundsParams a;
+    a.src = k_new;
+    a.s0 = kn_strides[0];
+    a.s1 = kn_strides[1];
+    a.s2 = 0;
+    a.slots = slots;
+    a.kmin = kmin;
+    a.kmax = kmax;
+    a.sb_b = bound_strides[0];
+    a.sb_h = bound_strides[1];
+    a.num_blocks = num_blocks;
+    a.B = batch;
+    a.H = kv_heads;
+    return hip_status(ls::launch_bounds_update(a, (hipStream_t)stream), "ls_page_bounds_update");
+}
+
+int ls_page_bounds_rebuild(const void* k_pool, const int64_t* kv_strides, int num_blocks,
+                           void* kmin, void* kmax, const int64_t* bound_strides, int kv_heads,
+                           int head_dim, int page, void* stream) {
+    if (!k_pool || !kv_strides || !kmin || !kmax || !bound_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim != ls::HEAD_DIM) return fail(LS_ERR_INVALID, "head_dim must be 128, got %d", head_dim);
+    if (page != ls::PAGE) return fail(LS_ERR_INVALID, "page (block_size) must be 16, got %d", page);
+    if (kv_heads < 1 || num_blocks < 0) return fail(LS_ERR_INVALID, "bad kv_heads or num_blocks");
+    if (!rows_aligned(k_pool, kv_strides, 3, 2, 16) || !rows_aligned(kmin, bound_strides, 2, 2, 16) ||
+        !rows_aligned(kmax, bound_strides, 2, 2, 16))
+        return fail(LS_ERR_INVALID, "k_pool, kmin and kmax rows must be 16-byte aligned");
+    ls::BoundsParams a;
+    a.src = k_pool;
+    a.s0 = kv_strides[0];
+    a.s1 = kv_strides[1];
+    a.s2 = kv_strides[2];
+    a.slots = nullptr;
+    a.kmin = kmin;
+    a.kmax = kmax;
+    a.sb_b = bound_strides[0];
+    a.sb_h = bound_strides[1];
+    a.num_blocks = num_blocks;
+    a.B = 0;
+    a.H = kv_heads;
+    return hip_status(ls::launch_bounds_rebuild(a, (hipStream_t)stream), "ls_page_bounds_rebuild");
 }
 
 }  // extern "C"

@@ -1,0 +1,455 @@
+// Page selection for sparse decode on gfx950: the page indexer (Quest upper
+// bound per page), top-k selection, and the per-page K bounds it reads.
+//
+// Reference: kernels/cuda/paged_sparse_fp16.cu:54-72 (page_bounds_update),
+// :78-130 (page_index), kernels/cuda/paged_sparse.py:81-123 (rebuild_bounds,
+// update_bounds, page_scores), :164-168 (select = torch.topk) and
+// :222-251 (sparse_attention: index -> select -> attend).
+//
+// Design:
+//  * Indexer: a wave scores 4 pages at a time, 16 lanes per page, 8 channels
+//    per lane (one 16-byte load of kmin and of kmax).  The per-head bound
+//    sum_d max(q_d * lo_d, q_d * hi_d) is formed in fp32 (each product of two
+//    fp16 values is exact in fp32) and reduced over the 16 lanes with four
+//    DPP adds; the page score is the max over the n_rep query heads.  The
+//    work is a pass over 2 x 256 bytes per (page, KV head): HBM-bound.
+//  * Selection: one 256-thread group per (sequence, KV head) holds the row's
+//    keys in registers (32 per thread), finds the n-th largest key by a
+//    4-pass radix select (8-bit digits, LDS histograms), and writes the
+//    selected page ids in page order.  Ties at the threshold are taken in
+//    page order, so the result is deterministic.  With a ratio the first
+//    n_b entries are the sequence's own budget (the rule the sparse decode
+//    kernel applies to the list), the rest of the k entries follow.
+//  * Fused index + select: every index group stores its 32 scores (one
+//    128-byte line) write-through and bumps a per-(sequence, head) arrival
+//    counter; the last group to arrive runs the selection over the row and
+//    resets the counter.  One launch per layer for the selector.
+#include "ls_common.h"
+#include "ls_sparse.h"
+
+namespace ls {
+
+namespace {
+
+enum : int { PG_SKIP = 0, PG_SCORE = 1, PG_FORCED = 2, PG_PAST = 3 };
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                         0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each row of 16 lanes, result in every lane of the row: quad
+// swaps (xor 1, xor 2), then half-row and row mirrors.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x140>(v);
+    return v;
+}
+
+// (Components are named, not indexed: subscripting a vector-typed reference
+// inside an unrolled loop lost all but the first component in this build.)
+__device__ __forceinline__ void h8_to_f8(u4 x, float* f) {
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const h2 t = __builtin_bit_cast(h2, w[i]);
+        f[2 * i] = (float)t.x;
+        f[2 * i + 1] = (float)t.y;
+    }
+}
+
+__device__ __forceinline__ void store_through(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Order-preserving map float -> uint32 (larger float, larger key); -0 and
+// +0 compare equal, as they do for the reference's torch.topk.
+__device__ __forceinline__ uint32_t order_key(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    u = u == 0x80000000u ? 0u : u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Pages a sequence of length L attends with this ratio: the rule of the
+// sparse decode kernel (paged_sparse_fp16.cu:242-247), capped at k.
+__device__ __forceinline__ int budget_pages(int L, int P, float ratio, int recent, int k) {
+    int pages = L > 0 ? (L + PAGE - 1) / PAGE : 0;
+    pages = pages < P ? pages : P;
+    if (!(ratio > 0.f)) return k;
+    int want;
+    if (ratio >= 1.f) {
+        want = pages;
+    } else {
+        want = (int)ceilf(ratio * (float)pages);
+        want = want > recent + 1 ? want : recent + 1;
+    }
+    want = want < pages ? want : pages;
+    return want < k ? want : k;
+}
+
+constexpr int SEL_THREADS = 256;
+constexpr int SEL_KPT = SELECT_MAX_PAGES / SEL_THREADS;   // keys per thread
+
+struct SelectSmem {
+    uint32_t hist[2][256];
+    uint32_t wsum[4];
+    int found[4];
+    int last;
+};
+
+// Inclusive prefix sum over the 256 threads of a group.
+__device__ __forceinline__ uint32_t group_scan(uint32_t v, uint32_t* wsum) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = (uint32_t)__builtin_amdgcn_ds_bpermute((lane - o) << 2, (int)v);
+        if (lane >= o) v += t;
+    }
+    if (lane == 63) wsum[wv] = v;
+    __syncthreads();
+    for (int w = 0; w < wv; ++w) v += wsum[w];
+    __syncthreads();
+    return v;
+}
+
+// Select from one row of P scores: out[0, n1) = the n1 best pages, out[n1,
+// n2) = the next n2 - n1 (n1 <= n2 <= P), each part in page order.  Order
+// among equal scores: lower page first.  With SORTED (n1 == n2) the n2 pages
+// are written best first instead.
+template <bool SORTED>
+__device__ void select_row(const float* srow, int P, int n1, int n2, int32_t* out,
+                           SelectSmem& sm, uint32_t* skeys) {
+    const int tid = threadIdx.x;
+    const int kpt = (P + SEL_THREADS - 1) / SEL_THREADS;
+    const int i0 = tid * kpt;
+    int cnt = P - i0;
+    cnt = cnt < 0 ? 0 : (cnt > kpt ? kpt : cnt);
+    uint32_t key[SEL_KPT];
+#pragma unroll
+    for (int j = 0; j < SEL_KPT; ++j) key[j] = j < cnt ? order_key(srow[i0 + j]) : 0u;
+
+    // ---- radix select of the n1-th and n2-th largest keys ----
+    uint32_t pre0 = 0, pre1 = 0, msk = 0;
+    int rem0 = n1, rem1 = n2;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        sm.hist[0][tid] = 0;
+        sm.hist[1][tid] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < SEL_KPT; ++j) {
+            if (j < cnt) {
+                const uint32_t d = (key[j] >> shift) & 255u;
+                if ((key[j] & msk) == pre0) atomicAdd(&sm.hist[0][d], 1u);
+                if ((key[j] & msk) == pre1) atomicAdd(&sm.hist[1][d], 1u);
+            }
+        }
+        __syncthreads();
+        const int bin = 255 - tid;   // thread order = descending digit
+        const uint32_t c = sm.hist[0][bin] | (sm.hist[1][bin] << 16);
+        const uint32_t incl = group_scan(c, sm.wsum);
+        const uint32_t excl = incl - c;
+        const int ci0 = (int)(incl & 0xFFFFu), ce0 = (int)(excl & 0xFFFFu);
+        const int ci1 = (int)(incl >> 16), ce1 = (int)(excl >> 16);
+        if (ce0 < rem0 && ci0 >= rem0) {
+            sm.found[0] = bin;
+            sm.found[1] = rem0 - ce0;
+        }
+        if (ce1 < rem1 && ci1 >= rem1) {
+            sm.found[2] = bin;
+            sm.found[3] = rem1 - ce1;
+        }
+        __syncthreads();
+        if (rem0 > 0) {
+            pre0 |= (uint32_t)sm.found[0] << shift;
+            rem0 = sm.found[1];
+        }
+        if (rem1 > 0) {
+            pre1 |= (uint32_t)sm.found[2] << shift;
+            rem1 = sm.found[3];
+        }
+        msk |= 255u << shift;
+        __syncthreads();
+    }
+    // threshold keys pre0 / pre1; rem0 / rem1 = how many keys equal to them
+    // belong to the set (the lowest pages first)
+    const bool want0 = n1 > 0, want1 = n2 > 0;
+
+    uint32_t e = 0;
+#pragma unroll
+    for (int j = 0; j < SEL_KPT; ++j)
+        if (j < cnt) e += (key[j] == pre0 ? 1u : 0u) + (key[j] == pre1 ? 0x10000u : 0u);
+    uint32_t incl = group_scan(e, sm.wsum);
+    uint32_t excl = incl - e;
+    int r0 = (int)(excl & 0xFFFFu), r1 = (int)(excl >> 16);
+    uint32_t ma = 0, mb = 0;
+#pragma unroll
+    for (int j = 0; j < SEL_KPT; ++j) {
+        if (j < cnt) {
+            bool a0, a1;
+            if (key[j] == pre0) {
+                a0 = want0 && r0 < rem0;
+                ++r0;
+            } else {
+                a0 = want0 && key[j] > pre0;
+            }
+            if (key[j] == pre1) {
+                a1 = want1 && r1 < rem1;
+                ++r1;
+            } else {
+                a1 = want1 && key[j] > pre1;
+            }
+            ma |= (a0 ? 1u : 0u) << j;
+            mb |= (a1 && !a0 ? 1u : 0u) << j;
+        }
+    }
+    const uint32_t ab = (uint32_t)__builtin_popcount(ma) | ((uint32_t)__builtin_popcount(mb) << 16);
+    incl = group_scan(ab, sm.wsum);
+    excl = incl - ab;
+    int pa = (int)(excl & 0xFFFFu), pb = n1 + (int)(excl >> 16);
+    if constexpr (!SORTED) {
+#pragma unroll
+        for (int j = 0; j < SEL_KPT; ++j) {
+            if ((ma >> j) & 1u) out[pa++] = i0 + j;
+            if ((mb >> j) & 1u) out[pb++] = i0 + j;
+        }
+    } else {
+        // the set, in page order, into LDS; then rank each member against it
+        int pos[SEL_KPT];
+#pragma unroll
+        for (int j = 0; j < SEL_KPT; ++j) {
+            pos[j] = pa;
+            if ((ma >> j) & 1u) skeys[pa++] = key[j];
+        }
+        __syncthreads();
+        int rank[SEL_KPT];
+#pragma unroll
+        for (int j = 0; j < SEL_KPT; ++j) rank[j] = 0;
+        for (int m = 0; m < n1; ++m) {
+            const uint32_t km = skeys[m];
+#pragma unroll
+            for (int j = 0; j < SEL_KPT; ++j)
+                rank[j] += (km > key[j] || (km == key[j] && m < pos[j])) ? 1 : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < SEL_KPT; ++j)
+            if ((ma >> j) & 1u) out[rank[j]] = i0 + j;
+    }
+}
+
+template <bool FUSED>
+__global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
+    __shared__ SelectSmem sm;
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int c0 = (lane & 15) * 8;
+    const int L = a.seq_lens[b];
+    const int np = L > 0 ? (L + PAGE - 1) / PAGE : 0;
+
+    // the two pages of this lane's row group: state and bounds
+    int pg[2], st[2];
+    u4 lo[2], hi[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int p = blockIdx.x * INDEX_PAGES_PER_GROUP + wv * 8 + i * 4 + (lane >> 4);
+        pg[i] = p;
+        lo[i] = u4{0u, 0u, 0u, 0u};
+        hi[i] = u4{0u, 0u, 0u, 0u};
+        if (p >= a.max_pages) {
+            st[i] = PG_SKIP;
+        } else if (p >= np) {
+            st[i] = PG_PAST;
+        } else if (p == 0 || p >= np - a.recent) {
+            st[i] = PG_FORCED;
+        } else {
+            const int blk = a.block_tables[(int64_t)b * a.sbt_b + p];
+            if ((unsigned)blk >= (unsigned)a.num_blocks) {
+                st[i] = PG_PAST;            // a block id outside the pool is never chosen
+            } else {
+                st[i] = PG_SCORE;
+                const int64_t off = (int64_t)blk * a.sb_b + (int64_t)h * a.sb_h + c0;
+                lo[i] = *(const u4*)((const half_t*)a.kmin + off);
+                hi[i] = *(const u4*)((const half_t*)a.kmax + off);
+            }
+        }
+    }
+    const half_t* qb = (const half_t*)a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + c0;
+    u4 qv[MAX_NREP];
+#pragma unroll
+    for (int r = 0; r < MAX_NREP; ++r)
+        if (r < a.NR) qv[r] = *(const u4*)(qb + (int64_t)r * a.sq_r);
+
+    float best[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        float lf[8], hf[8];
+        h8_to_f8(lo[i], lf);
+        h8_to_f8(hi[i], hf);
+        float bst = neg_inf();
+#pragma unroll
+        for (int r = 0; r < MAX_NREP; ++r) {
+            if (r < a.NR) {                 // uniform over the group
+                float qf[8];
+                h8_to_f8(qv[r], qf);
+                float s = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) s += fmaxf(qf[j] * lf[j], qf[j] * hf[j]);
+                s = row16_sum(s);
+                bst = fmaxf(bst, s);
+            }
+        }
+        best[i] = bst;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if ((lane & 15) == 0 && st[i] != PG_SKIP) {
+            const float v = st[i] == PG_SCORE ? best[i]
+                            : st[i] == PG_FORCED ? __builtin_inff() : neg_inf();
+            float* dst = a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h + pg[i];
+            if (FUSED)
+                store_through(dst, v);
+            else
+                *dst = v;
+        }
+    }
+    if constexpr (FUSED) {
+        // scores written through to memory before the arrival is counted
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();
+        const int64_t bh = (int64_t)b * a.H + h;
+        if (threadIdx.x == 0) {
+            const int prev = __hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+            sm.last = prev == (int)gridDim.x - 1;
+        }
+        __syncthreads();
+        if (!sm.last) return;
+        // Every line of the row was written through by its group and none was
+        // read in this launch, so plain loads see the stored scores.
+        const int n1 = budget_pages(L, a.max_pages, a.ratio, a.recent, a.k);
+        select_row<false>(a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h, a.max_pages, n1,
+                          a.k, a.sel + (int64_t)b * a.sl_b + (int64_t)h * a.sl_h, sm, nullptr);
+        if (threadIdx.x == 0)
+            __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <bool SORTED>
+__global__ __launch_bounds__(256) void page_select_kernel(SelectParams a) {
+    __shared__ SelectSmem sm;
+    __shared__ uint32_t skeys[SORTED ? SELECT_MAX_PAGES : 1];
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int L = a.seq_lens ? a.seq_lens[b] : 0;
+    const int n1 = SORTED ? a.k : budget_pages(L, a.P, a.ratio, a.recent, a.k);
+    select_row<SORTED>(a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h, a.P, n1, a.k,
+                       a.sel + (int64_t)b * a.sl_b + (int64_t)h * a.sl_h, sm, skeys);
+}
+
+// grid (B, H), 64 threads: two channels per lane.
+__global__ __launch_bounds__(64) void bounds_update_kernel(BoundsParams a) {
+    const int b = blockIdx.x, h = blockIdx.y, c = threadIdx.x * 2;
+    const int64_t slot = a.slots[b];
+    if (slot < 0) return;
+    const int64_t blk = slot / PAGE;
+    const int off = (int)(slot % PAGE);
+    if (blk >= a.num_blocks) return;
+    const h2 v = *(const h2*)((const half_t*)a.src + (int64_t)b * a.s0 + (int64_t)h * a.s1 + c);
+    const int64_t i = blk * a.sb_b + (int64_t)h * a.sb_h + c;
+    h2* mn = (h2*)((half_t*)a.kmin + i);
+    h2* mx = (h2*)((half_t*)a.kmax + i);
+    if (off == 0) {                     // a page's first token resets its bounds
+        *mn = v;
+        *mx = v;
+        return;
+    }
+    const h2 m0 = *mn, x0 = *mx;        // fp16 min / max through fp32 are exact
+    h2 rn, rx;
+    rn.x = (half_t)fminf((float)m0.x, (float)v.x);
+    rn.y = (half_t)fminf((float)m0.y, (float)v.y);
+    rx.x = (half_t)fmaxf((float)x0.x, (float)v.x);
+    rx.y = (half_t)fmaxf((float)x0.y, (float)v.y);
+    *mn = rn;
+    *mx = rx;
+}
+
+// One (block, head) per 16 lanes, 8 channels per lane, all 16 rows.
+__global__ __launch_bounds__(256) void bounds_rebuild_kernel(BoundsParams a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t item = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
+    if (item >= (int64_t)a.num_blocks * a.H) return;
+    const int64_t blk = item / a.H;
+    const int h = (int)(item % a.H);
+    const int c0 = (lane & 15) * 8;
+    const half_t* src = (const half_t*)a.src + blk * a.s0 + (int64_t)h * a.s2 + c0;
+    u4 rows[PAGE];
+#pragma unroll
+    for (int t = 0; t < PAGE; ++t) rows[t] = stream_load((const u4*)(src + (int64_t)t * a.s1));
+    float mn[8], mx[8];
+    h8_to_f8(rows[0], mn);
+    h8_to_f8(rows[0], mx);
+#pragma unroll
+    for (int t = 1; t < PAGE; ++t) {
+        float f[8];
+        h8_to_f8(rows[t], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            mn[j] = fminf(mn[j], f[j]);
+            mx[j] = fmaxf(mx[j], f[j]);
+        }
+    }
+    uint32_t wn[4], wx[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h2 a2 = {(half_t)mn[2 * i], (half_t)mn[2 * i + 1]};
+        h2 b2 = {(half_t)mx[2 * i], (half_t)mx[2 * i + 1]};
+        wn[i] = __builtin_bit_cast(uint32_t, a2);
+        wx[i] = __builtin_bit_cast(uint32_t, b2);
+    }
+    const u4 omn = {wn[0], wn[1], wn[2], wn[3]};
+    const u4 omx = {wx[0], wx[1], wx[2], wx[3]};
+    const int64_t o = blk * a.sb_b + (int64_t)h * a.sb_h + c0;
+    *(u4*)((half_t*)a.kmin + o) = omn;
+    *(u4*)((half_t*)a.kmax + o) = omx;
+}
+
+}  // namespace
+
+hipError_t launch_page_index(const IndexParams& p, hipStream_t stream) {
+    if (p.B == 0 || p.max_pages == 0) return hipSuccess;
+    const dim3 grid((p.max_pages + INDEX_PAGES_PER_GROUP - 1) / INDEX_PAGES_PER_GROUP, p.H, p.B);
+    if (p.sel)
+        hipLaunchKernelGGL(page_index_kernel<true>, grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(page_index_kernel<false>, grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_page_select(const SelectParams& p, hipStream_t stream) {
+    if (p.B == 0 || p.k == 0) return hipSuccess;
+    const dim3 grid(p.H, p.B);
+    if (p.sorted)
+        hipLaunchKernelGGL(page_select_kernel<true>, grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(page_select_kernel<false>, grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_bounds_update(const BoundsParams& p, hipStream_t stream) {
+    if (p.B == 0) return hipSuccess;
+    hipLaunchKernelGGL(bounds_update_kernel, dim3(p.B, p.H), dim3(64), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_bounds_rebuild(const BoundsParams& p, hipStream_t stream) {
+    const int64_t items = (int64_t)p.num_blocks * p.H;
+    if (items == 0) return hipSuccess;
+    const int64_t groups = (items * 16 + 255) / 256;
+    hipLaunchKernelGGL(bounds_rebuild_kernel, dim3((unsigned)groups), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace ls

@@ -1,25 +1,163 @@
 """Sparse (page-subset) decode attention on the HIP kernels.
 
 Mirrors the reference's kernels/cuda/paged_sparse.py: ``budget`` (:74-78),
-``budgets`` (:171-182), ``select`` (:164-168), ``sparse_decode`` (:185-219)
-and ``sparse_attention`` (:222-251), with ``page_scores`` / ``update_bounds``
-/ ``rebuild_bounds`` on HIP kernels of their own.
+``rebuild_bounds`` (:81-84), ``update_bounds`` (:86-101), ``page_scores``
+(:104-123), ``select`` (:164-168), ``budgets`` (:171-182), ``sparse_decode``
+(:185-219) and ``sparse_attention`` (:222-251), all on HIP kernels.
 
-Per layer per decode step the pipeline is index -> top-k -> attend, all on
-the GPU and capturable in a HIP graph.
+Per layer per decode step the pipeline is two launches: index + select
+(one fused kernel: the last index group of each (sequence, head) selects)
+and the page-subset decode. Nothing syncs with the host, so the step is
+capturable in a HIP graph.
 """
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional
 
 import torch
 
 from latentserve_amd import _lib
+from latentserve_amd.kernels.gqa import _scratch as scratch
 from latentserve_amd.kernels.hip import paged_decode_hip as pdh
 
 PAGE = pdh.PAGE
+SELECT_MAX_PAGES = 8192
+_LINE_FLOATS = 32          # one 128-byte line of fp32 scores per index group
+
+
+def _check_bounds(kmin: torch.Tensor, kmax: torch.Tensor, device) -> None:
+    if kmin.dtype != torch.float16 or kmax.dtype != torch.float16:
+        raise ValueError("kmin/kmax must be float16 [num_blocks, H_kv, head_dim]")
+    if kmin.dim() != 3 or kmin.shape != kmax.shape or kmin.stride() != kmax.stride() \
+            or kmin.stride(-1) != 1:
+        raise ValueError("kmin/kmax must match, [num_blocks, H_kv, head_dim], unit last stride")
+    if kmin.device != device or kmax.device != device:
+        raise ValueError("kmin/kmax must be on q's device")
+
+
+def _score_buffer(b: int, h: int, max_pages: int, device) -> torch.Tensor:
+    """Persistent [B, H, max_pages] fp32 view whose rows start on 128-byte
+    lines (the fused index+select kernel's requirement)."""
+    width = -(-max(1, max_pages) // _LINE_FLOATS) * _LINE_FLOATS
+    buf = scratch("sparse_scores", (b, h, width), torch.float32, device)
+    return buf[:, :, :max_pages]
+
+
+def rebuild_bounds(k_pool: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor) -> None:
+    """Every block's per-channel K bounds from the pool, over all PAGE rows."""
+    _check_bounds(kmin, kmax, k_pool.device)
+    if k_pool.dtype != torch.float16 or k_pool.stride(-1) != 1:
+        raise ValueError("k_pool must be float16 with unit last stride")
+    nb, page, h, d = k_pool.shape
+    if kmin.shape != (nb, h, d):
+        raise ValueError(f"kmin/kmax must be [{nb}, {h}, {d}]")
+    P, S = _lib.ptr, _lib.strides
+    rc = _lib.lib().ls_page_bounds_rebuild(P(k_pool), S(k_pool, 3), nb, P(kmin), P(kmax),
+                                           S(kmin, 2), h, d, page, _lib.stream_of(k_pool.device))
+    _lib.check(rc, "ls_page_bounds_rebuild")
+
+
+def update_bounds(k_new: torch.Tensor, slots: torch.Tensor, kmin: torch.Tensor,
+                  kmax: torch.Tensor, page: int = 16) -> None:
+    """k_new [B, H, D] (or [B, H, 1, D]) just written at flat `slots` [B]."""
+    k = k_new.reshape(k_new.shape[0], k_new.shape[1], k_new.shape[-1])
+    _check_bounds(kmin, kmax, k.device)
+    if k.dtype != torch.float16 or k.stride(-1) != 1:
+        raise ValueError("k_new must be float16 with unit last stride")
+    if slots.dtype != torch.int64 or slots.dim() != 1 or slots.shape[0] != k.shape[0] \
+            or slots.stride(0) != 1:
+        raise ValueError("slots must be a contiguous int64 [B] tensor")
+    b, h, d = k.shape
+    P, S = _lib.ptr, _lib.strides
+    rc = _lib.lib().ls_page_bounds_update(P(k), S(k, 2), P(slots), P(kmin), P(kmax), S(kmin, 2),
+                                          kmin.shape[0], b, h, d, page,
+                                          _lib.stream_of(k.device))
+    _lib.check(rc, "ls_page_bounds_update")
+
+
+def _check_index_inputs(q, kmin, kmax, block_tables, seq_lens):
+    if q.dtype != torch.float16 or q.dim() != 4 or q.stride(-1) != 1:
+        raise ValueError("q must be float16 [B, H_kv, n_rep, D] with unit last stride")
+    _check_bounds(kmin, kmax, q.device)
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32 \
+            or block_tables.stride(-1) != 1 or seq_lens.stride(-1) != 1:
+        raise ValueError("block tables and sequence lengths must be unit-stride int32")
+
+
+def page_scores(q, kmin, kmax, block_tables, seq_lens, recent: int = 2) -> torch.Tensor:
+    """-> [B, H, max_pages] fp32: bound per page, +inf forced, -inf past the end."""
+    _check_index_inputs(q, kmin, kmax, block_tables, seq_lens)
+    b, h, n_rep, d = q.shape
+    max_pages = block_tables.shape[1]
+    scores = _score_buffer(b, h, max_pages, q.device)
+    P, S = _lib.ptr, _lib.strides
+    rc = _lib.lib().ls_page_scores(
+        P(q), S(q, 3), P(kmin), P(kmax), S(kmin, 2), kmin.shape[0], P(block_tables),
+        block_tables.stride(0), max_pages, P(seq_lens), P(scores), S(scores, 2),
+        b, h, n_rep, d, PAGE, int(recent), _lib.stream_of(q.device))
+    _lib.check(rc, "ls_page_scores")
+    return scores
+
+
+def select(scores: torch.Tensor, k: int, sorted: bool = False,
+           seq_lens: Optional[torch.Tensor] = None, ratio: Optional[float] = None,
+           recent: int = 2) -> torch.Tensor:
+    """Top-k pages per (sequence, head) -> int32 [B, H, k].
+
+    Ties between equal scores go to the lower page. ``sorted``: best first
+    (forced +inf pages first, then by score). Unsorted, the pages come in
+    page order; given ``seq_lens`` and ``ratio``, the first n_b entries of
+    sequence b are then its own budget's best pages (what sparse_decode
+    attends with that ratio) and the remaining k - n_b follow.
+    """
+    if scores.dtype != torch.float32 or scores.dim() != 3 or scores.stride(-1) != 1:
+        raise ValueError("scores must be float32 [B, H, P] with unit last stride")
+    b, h, p = scores.shape
+    k = int(k)
+    if not 0 <= k <= p:
+        raise ValueError(f"k={k} out of range for {p} pages")
+    if p > SELECT_MAX_PAGES:
+        raise ValueError(f"select supports up to {SELECT_MAX_PAGES} pages, got {p}")
+    use_ratio = ratio is not None and not sorted
+    if use_ratio and (seq_lens is None or seq_lens.dtype != torch.int32):
+        raise ValueError("a ratio needs int32 seq_lens")
+    if k == 0 or b == 0:
+        return torch.empty(b, h, k, dtype=torch.int32, device=scores.device)
+    sel = scratch("sparse_select", (b, h, k), torch.int32, scores.device)
+    P, S = _lib.ptr, _lib.strides
+    rc = _lib.lib().ls_page_select(
+        P(scores), S(scores, 2), P(seq_lens) if use_ratio else None, b, h, p, k,
+        float(ratio) if use_ratio else 0.0, int(recent), 1 if sorted else 0, P(sel),
+        (ctypes.c_int64 * 2)(*sel.stride()[:2]), _lib.stream_of(scores.device))
+    _lib.check(rc, "ls_page_select")
+    return sel
+
+
+def index_select(q, kmin, kmax, block_tables, seq_lens, k: int, ratio: float,
+                 recent: int = 2) -> torch.Tensor:
+    """page_scores + select(ratio=...) in one launch -> int32 [B, H, k]."""
+    _check_index_inputs(q, kmin, kmax, block_tables, seq_lens)
+    b, h, n_rep, d = q.shape
+    max_pages = block_tables.shape[1]
+    if max_pages > SELECT_MAX_PAGES:
+        raise ValueError(f"selection supports up to {SELECT_MAX_PAGES} pages, got {max_pages}")
+    k = int(k)
+    if not 1 <= k <= max_pages:
+        raise ValueError(f"k={k} out of range for {max_pages} pages")
+    scores = _score_buffer(b, h, max_pages, q.device)
+    sel = scratch("sparse_index_sel", (b, h, k), torch.int32, q.device)
+    cnt = scratch("sparse_index_cnt", (b * h,), torch.int32, q.device, init=0)
+    P, S = _lib.ptr, _lib.strides
+    rc = _lib.lib().ls_sparse_index(
+        P(q), S(q, 3), P(kmin), P(kmax), S(kmin, 2), kmin.shape[0], P(block_tables),
+        block_tables.stride(0), max_pages, P(seq_lens), P(scores), S(scores, 2), P(cnt), k,
+        float(ratio), int(recent), P(sel), S(sel, 2), b, h, n_rep, d, PAGE,
+        _lib.stream_of(q.device))
+    _lib.check(rc, "ls_sparse_index")
+    return sel
 
 
 def budget(ratio: float, max_pages: int, recent: int = 2) -> int:
@@ -74,3 +212,23 @@ def sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel,
         splits, 0, float(scale), _lib.stream_of(q.device))
     _lib.check(rc, "ls_paged_sparse_fp16")
     return out[:, :, :n_rep]
+
+
+def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
+                     ratio: float = 0.25, recent: int = 2,
+                     num_splits: Optional[int] = None, max_seq_len: Optional[int] = None,
+                     softmax_scale: Optional[float] = None,
+                     scoring: str = "bounds") -> torch.Tensor:
+    """Index, select, attend (two launches). The list width k follows
+    `max_seq_len` (the context) when given, else the table's width; each
+    sequence then attends its own budget for its current length."""
+    if scoring != "bounds":
+        raise ValueError(f"scoring {scoring!r} is not provided by the HIP backend "
+                         "(only 'bounds')")
+    page = k_pool.shape[1]
+    pages = block_tables.shape[1] if max_seq_len is None else min(
+        block_tables.shape[1], -(-int(max_seq_len) // page))
+    k = budget(ratio, pages, recent)
+    sel = index_select(q, kmin, kmax, block_tables, seq_lens, k, ratio, recent)
+    return sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel, num_splits,
+                         softmax_scale, ratio=ratio, recent=recent)

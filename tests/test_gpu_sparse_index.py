@@ -1,0 +1,254 @@
+"""HIP page selection (indexer, top-k, bounds) against the CPU oracle, on an
+MI355X.
+
+Selection is integer work on given scores: ``select`` is compared
+entry-for-entry with the oracle's stable descending sort (ties -> lower page,
+the rule both sides document; the reference's torch.topk leaves tie order
+open).  Scores are fp32 sums of exact fp16 products whose summation order
+differs from the oracle's, so they are compared at rtol 1e-5, and the
+selection the GPU makes from its own scores is compared as a *set* with the
+oracle's, allowing swaps only across a score gap below 1e-4 relative (the
+reference's own indexer test tolerance, tests/test_phase14_sparse_kernels.py:
+92-107).  Bounds are fp16 min/max: bit-exact.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.cases import assert_close, paged_case
+
+torch = pytest.importorskip("torch")
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def dev(*arrays):
+    return [None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in arrays]
+
+
+def ps():
+    from latentserve_amd.kernels.hip import paged_sparse
+    return paged_sparse
+
+
+def bounds_of(k_pool):
+    return k_pool.min(axis=1), k_pool.max(axis=1)
+
+
+def index_case(lengths, width=None, n_rep=6, seed=0, h_kv=2):
+    q, k, v, t, l = paged_case(lengths, h_kv=h_kv, n_rep=n_rep, seed=seed, width=width)
+    kmin, kmax = bounds_of(k)
+    return q, k, v, t, l, np.ascontiguousarray(kmin), np.ascontiguousarray(kmax)
+
+
+def sets_agree(got, want, scores, k_rows, tol=1e-4):
+    """got/want: selected page lists per (b, h); disagreements only where the
+    oracle's scores of the swapped pages sit within tol of the threshold."""
+    b, h = scores.shape[:2]
+    for i in range(b):
+        for j in range(h):
+            g, w = set(got[i][j]), set(want[i][j])
+            if g == w:
+                continue
+            thr = min(scores[i, j, p] for p in w) if w else 0.0
+            for p in g ^ w:
+                s = scores[i, j, p]
+                assert np.isfinite(s) and abs(s - thr) <= tol * max(1.0, abs(thr)), \
+                    (i, j, p, s, thr)
+
+
+# ------------------------------------------------------------- scores ----
+@pytest.mark.parametrize("n_rep", [1, 6, 16])
+def test_page_scores_match_the_oracle(n_rep):
+    q, k, v, t, l, kmin, kmax = index_case([2048 + 5, 700, 33, 1, 0], width=200, n_rep=n_rep)
+    want = oracle.page_scores(q, kmin, kmax, t, l, recent=2)
+    Q, KN, KX, T, L = dev(q, kmin, kmax, t, l)
+    got = ps().page_scores(Q, KN, KX, T, L, recent=2).cpu().numpy()
+    assert got.shape == want.shape
+    assert np.array_equal(np.isposinf(got), np.isposinf(want))
+    assert np.array_equal(np.isneginf(got), np.isneginf(want))
+    fin = np.isfinite(want)
+    assert np.allclose(got[fin], want[fin], rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("recent", [0, 1, 2, 5])
+def test_forced_pages_follow_recent(recent):
+    q, k, v, t, l, kmin, kmax = index_case([40 * 16 + 3, 16 * 7], width=48)
+    Q, KN, KX, T, L = dev(q, kmin, kmax, t, l)
+    got = ps().page_scores(Q, KN, KX, T, L, recent=recent).cpu().numpy()
+    for b, n in enumerate([41, 7]):
+        forced = {0} | set(range(max(0, n - recent), n))
+        assert set(np.flatnonzero(np.isposinf(got[b, 0]))) == forced
+        assert set(np.flatnonzero(np.isneginf(got[b, 0]))) == set(range(n, 48))
+
+
+def test_block_ids_outside_the_pool_score_minus_inf():
+    q, k, v, t, l, kmin, kmax = index_case([64 * 16], width=64)
+    t = t.copy()
+    t[0, 10] = 10 ** 6
+    t[0, 11] = -3
+    Q, KN, KX, T, L = dev(q, kmin, kmax, t, l)
+    got = ps().page_scores(Q, KN, KX, T, L).cpu().numpy()
+    assert np.isneginf(got[0, :, 10]).all() and np.isneginf(got[0, :, 11]).all()
+    assert np.isfinite(got[0, :, 12]).all()
+
+
+# ------------------------------------------------------------- select ----
+def random_scores(b, h, p, seed, ties=False):
+    rng = np.random.default_rng(seed)
+    s = rng.standard_normal((b, h, p)).astype(np.float32)
+    if ties:
+        s = np.round(s * 2) / 2          # a handful of distinct values, many ties
+    s[:, :, 0] = np.inf
+    s[:, :, -3:] = -np.inf
+    return s
+
+
+@pytest.mark.parametrize("p,k", [(1, 1), (37, 5), (200, 200), (2048, 1024), (8192, 4000)])
+@pytest.mark.parametrize("ties", [False, True])
+def test_select_sorted_equals_the_oracle(p, k, ties):
+    s = random_scores(3, 2, p, seed=p + k, ties=ties)
+    got = ps().select(dev(s)[0], k, sorted=True).cpu().numpy()
+    assert np.array_equal(got, oracle.select(s, k))
+
+
+@pytest.mark.parametrize("p,k", [(37, 5), (2048, 1024), (1000, 999)])
+def test_select_unsorted_is_the_top_k_in_page_order(p, k):
+    s = random_scores(2, 2, p, seed=k, ties=True)
+    got = ps().select(dev(s)[0], k).cpu().numpy()
+    want = np.sort(oracle.select(s, k), axis=-1)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("ratio", [0.25, 0.5, 0.9])
+def test_select_ratio_puts_each_sequences_budget_first(ratio):
+    p = 512
+    lens = np.array([p * 16, 300 * 16 + 1, 17, 0, 3 * 16], dtype=np.int32)
+    s = random_scores(len(lens), 2, p, seed=3, ties=True)
+    k = ps().budget(ratio, p)
+    got = ps().select(dev(s)[0], k, seq_lens=dev(lens)[0], ratio=ratio).cpu().numpy()
+    full = oracle.select(s, k)
+    for b, length in enumerate(lens):
+        pages = min(p, (int(length) + 15) // 16)
+        n = oracle.sparse_count(pages, k, ratio, 2)
+        for h in range(2):
+            assert np.array_equal(got[b, h, :n], np.sort(full[b, h, :n])), (b, h)
+            assert np.array_equal(got[b, h, n:], np.sort(full[b, h, n:k])), (b, h)
+
+
+def test_select_zero_k_and_errors():
+    s = dev(random_scores(1, 1, 10, 0))[0]
+    assert ps().select(s, 0).shape == (1, 1, 0)
+    with pytest.raises(ValueError):
+        ps().select(s, 11)
+
+
+# ------------------------------------------------------- fused index -----
+@pytest.mark.parametrize("width", [200, 33, 2048])
+def test_fused_index_select_equals_scores_then_select(width):
+    lens = [width * 16, width * 8 + 3, 100, 1]
+    q, k, v, t, l, kmin, kmax = index_case(lens, width=width, seed=width)
+    Q, KN, KX, T, L = dev(q, kmin, kmax, t, l)
+    kk = ps().budget(0.5, width)
+    for _ in range(3):      # the arrival counters must come back to zero every call
+        fused = ps().index_select(Q, KN, KX, T, L, kk, 0.5).cpu().numpy()
+        scores = ps().page_scores(Q, KN, KX, T, L)
+        split = ps().select(scores, kk, seq_lens=L, ratio=0.5).cpu().numpy()
+        assert np.array_equal(fused, split)
+
+
+def test_gpu_selection_agrees_with_the_oracle_selection():
+    width = 512
+    lens = [width * 16, 5000, 777]
+    q, k, v, t, l, kmin, kmax = index_case(lens, width=width, seed=9)
+    Q, KN, KX, T, L = dev(q, kmin, kmax, t, l)
+    kk = ps().budget(0.5, width)
+    got = ps().index_select(Q, KN, KX, T, L, kk, 0.5).cpu().numpy()
+    scores = oracle.page_scores(q, kmin, kmax, t, l)
+    full = oracle.select(scores, kk)
+    g, w = [], []
+    for b, length in enumerate(lens):
+        n = oracle.sparse_count((length + 15) // 16, kk, 0.5, 2)
+        g.append([got[b, h, :n] for h in range(2)])
+        w.append([full[b, h, :n] for h in range(2)])
+    sets_agree(g, w, scores, None)
+
+
+# --------------------------------------------------- sparse attention ----
+@pytest.mark.parametrize("ratio", [0.25, 0.5, 1.0])
+def test_sparse_attention_end_to_end(ratio):
+    width = 256
+    lens = [width * 16, 2500, 700, 40]
+    q, k, v, t, l, kmin, kmax = index_case(lens, width=width, seed=int(ratio * 8))
+    Q, K, V, T, L, KN, KX = dev(q, k, v, t, l, kmin, kmax)
+    out = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=ratio).float().cpu().numpy()
+    kk = ps().budget(ratio, width)
+    sel = ps().index_select(Q, KN, KX, T, L, kk, ratio).cpu().numpy()
+    want = oracle.sparse_decode(q, k, v, t, l, sel, ratio=ratio, recent=2)
+    assert_close(out, want, ATOL, RTOL, f"ratio={ratio}")
+    if ratio >= 1.0:
+        assert_close(out, oracle.paged_decode(q, k, v, t, l), ATOL, RTOL, "full = dense")
+
+
+def test_sparse_attention_graph_replays():
+    width = 128
+    q, k, v, t, l, kmin, kmax = index_case([width * 16, 900], width=width, seed=4)
+    Q, K, V, T, L, KN, KX = dev(q, k, v, t, l, kmin, kmax)
+    eager = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=0.5).clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=0.5)
+    for i in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        ps().page_scores(Q, KN, KX, T, L)      # eager work between replays
+        torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------- bounds ----
+def test_rebuild_bounds_is_exact():
+    _, k, _, _, _ = paged_case([300], seed=2)
+    K = dev(k)[0]
+    kmin = torch.empty(k.shape[0], k.shape[2], k.shape[3], dtype=torch.float16, device="cuda")
+    kmax = torch.empty_like(kmin)
+    ps().rebuild_bounds(K, kmin, kmax)
+    lo, hi = bounds_of(k)
+    assert np.array_equal(kmin.cpu().numpy().view(np.uint16), lo.view(np.uint16))
+    assert np.array_equal(kmax.cpu().numpy().view(np.uint16), hi.view(np.uint16))
+
+
+def test_update_bounds_is_bit_exact_over_a_decode_stream():
+    rng = np.random.default_rng(5)
+    nb, h, d, b = 12, 2, 128, 3
+    kmin = rng.standard_normal((nb, h, d)).astype(np.float16)
+    kmax = kmin.copy()
+    KN, KX = dev(kmin, kmax)
+    starts = np.array([0, 4 * 16 + 9, 9 * 16], dtype=np.int64)   # a mid-page start too
+    for step in range(20):
+        k_new = rng.standard_normal((b, h, d)).astype(np.float16)
+        slots = starts + step
+        oracle.bounds_update(k_new, slots, kmin, kmax)
+        kn, sl = dev(k_new, slots)
+        ps().update_bounds(kn, sl, KN, KX)
+    torch.cuda.synchronize()
+    assert np.array_equal(KN.cpu().numpy().view(np.uint16), kmin.view(np.uint16))
+    assert np.array_equal(KX.cpu().numpy().view(np.uint16), kmax.view(np.uint16))
+
+
+def test_update_bounds_skips_slots_outside_the_pool():
+    kmin = torch.zeros(2, 1, 128, dtype=torch.float16, device="cuda")
+    kmax = torch.zeros_like(kmin)
+    k_new = torch.ones(2, 1, 128, dtype=torch.float16, device="cuda")
+    slots = torch.tensor([2 * 16, -1], dtype=torch.int64, device="cuda")
+    ps().update_bounds(k_new, slots, kmin, kmax)
+    torch.cuda.synchronize()
+    assert kmin.abs().sum().item() == 0 and kmax.abs().sum().item() == 0
