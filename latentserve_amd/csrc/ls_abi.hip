@@ -8,6 +8,7 @@
 // y dimension is the batch.
 
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 

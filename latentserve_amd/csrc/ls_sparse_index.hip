@@ -119,17 +119,27 @@ __device__ __forceinline__ uint32_t group_scan(uint32_t v, uint32_t* wsum) {
 // n2) = the next n2 - n1 (n1 <= n2 <= P), each part in page order.  Order
 // among equal scores: lower page first.  With SORTED (n1 == n2) the n2 pages
 // are written best first instead.
-template <bool SORTED>
-__device__ void select_row(const float* srow, int P, int n1, int n2, int32_t* out,
-                           SelectSmem& sm, uint32_t* skeys) {
+//
+// KPT keys per thread (P <= 256 * KPT): the loops over a thread's keys are
+// fully unrolled at exactly KPT, so their cost follows the row length.
+template <bool SORTED, int KPT>
+__device__ __attribute__((always_inline)) void select_row_k(const float* srow, int P, int n1,
+                                                            int n2, int32_t* out, SelectSmem& sm,
+                                                            uint32_t* skeys) {
     const int tid = threadIdx.x;
-    const int kpt = (P + SEL_THREADS - 1) / SEL_THREADS;
-    const int i0 = tid * kpt;
+    const int i0 = tid * KPT;
     int cnt = P - i0;
-    cnt = cnt < 0 ? 0 : (cnt > kpt ? kpt : cnt);
-    uint32_t key[SEL_KPT];
+    cnt = cnt < 0 ? 0 : (cnt > KPT ? KPT : cnt);
+    uint32_t key[KPT];
+    {
+        // unconditional loads (clamped index) so they all issue back to back
+        float f[KPT];
+        const int last = P > 0 ? P - 1 : 0;
 #pragma unroll
-    for (int j = 0; j < SEL_KPT; ++j) key[j] = j < cnt ? order_key(srow[i0 + j]) : 0u;
+        for (int j = 0; j < KPT; ++j) f[j] = P > 0 ? srow[i0 + j < last ? i0 + j : last] : 0.f;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) key[j] = j < cnt ? order_key(f[j]) : 0u;
+    }
 
     // ---- radix select of the n1-th and n2-th largest keys ----
     uint32_t pre0 = 0, pre1 = 0, msk = 0;
@@ -138,14 +148,35 @@ __device__ void select_row(const float* srow, int P, int n1, int n2, int32_t* ou
         sm.hist[0][tid] = 0;
         sm.hist[1][tid] = 0;
         __syncthreads();
+        // A thread's keys are adjacent pages whose leading digits mostly
+        // agree (one exponent for the whole row): count runs of equal digits
+        // and add each run once, instead of one LDS atomic per key on a
+        // handful of hot bins.
+        uint32_t d0 = 256u, n0 = 0u, d1 = 256u, n1c = 0u;
 #pragma unroll
-        for (int j = 0; j < SEL_KPT; ++j) {
+        for (int j = 0; j < KPT; ++j) {
             if (j < cnt) {
                 const uint32_t d = (key[j] >> shift) & 255u;
-                if ((key[j] & msk) == pre0) atomicAdd(&sm.hist[0][d], 1u);
-                if ((key[j] & msk) == pre1) atomicAdd(&sm.hist[1][d], 1u);
+                if ((key[j] & msk) == pre0) {
+                    if (d != d0) {
+                        if (n0) atomicAdd(&sm.hist[0][d0], n0);
+                        d0 = d;
+                        n0 = 0u;
+                    }
+                    ++n0;
+                }
+                if ((key[j] & msk) == pre1) {
+                    if (d != d1) {
+                        if (n1c) atomicAdd(&sm.hist[1][d1], n1c);
+                        d1 = d;
+                        n1c = 0u;
+                    }
+                    ++n1c;
+                }
             }
         }
+        if (n0) atomicAdd(&sm.hist[0][d0], n0);
+        if (n1c) atomicAdd(&sm.hist[1][d1], n1c);
         __syncthreads();
         const int bin = 255 - tid;   // thread order = descending digit
         const uint32_t c = sm.hist[0][bin] | (sm.hist[1][bin] << 16);
@@ -179,14 +210,14 @@ __device__ void select_row(const float* srow, int P, int n1, int n2, int32_t* ou
 
     uint32_t e = 0;
 #pragma unroll
-    for (int j = 0; j < SEL_KPT; ++j)
+    for (int j = 0; j < KPT; ++j)
         if (j < cnt) e += (key[j] == pre0 ? 1u : 0u) + (key[j] == pre1 ? 0x10000u : 0u);
     uint32_t incl = group_scan(e, sm.wsum);
     uint32_t excl = incl - e;
     int r0 = (int)(excl & 0xFFFFu), r1 = (int)(excl >> 16);
     uint32_t ma = 0, mb = 0;
 #pragma unroll
-    for (int j = 0; j < SEL_KPT; ++j) {
+    for (int j = 0; j < KPT; ++j) {
         if (j < cnt) {
             bool a0, a1;
             if (key[j] == pre0) {
@@ -211,32 +242,51 @@ __device__ void select_row(const float* srow, int P, int n1, int n2, int32_t* ou
     int pa = (int)(excl & 0xFFFFu), pb = n1 + (int)(excl >> 16);
     if constexpr (!SORTED) {
 #pragma unroll
-        for (int j = 0; j < SEL_KPT; ++j) {
+        for (int j = 0; j < KPT; ++j) {
             if ((ma >> j) & 1u) out[pa++] = i0 + j;
             if ((mb >> j) & 1u) out[pb++] = i0 + j;
         }
     } else {
         // the set, in page order, into LDS; then rank each member against it
-        int pos[SEL_KPT];
+        int pos[KPT];
 #pragma unroll
-        for (int j = 0; j < SEL_KPT; ++j) {
+        for (int j = 0; j < KPT; ++j) {
             pos[j] = pa;
             if ((ma >> j) & 1u) skeys[pa++] = key[j];
         }
         __syncthreads();
-        int rank[SEL_KPT];
+        int rank[KPT];
 #pragma unroll
-        for (int j = 0; j < SEL_KPT; ++j) rank[j] = 0;
+        for (int j = 0; j < KPT; ++j) rank[j] = 0;
         for (int m = 0; m < n1; ++m) {
             const uint32_t km = skeys[m];
 #pragma unroll
-            for (int j = 0; j < SEL_KPT; ++j)
+            for (int j = 0; j < KPT; ++j)
                 rank[j] += (km > key[j] || (km == key[j] && m < pos[j])) ? 1 : 0;
         }
 #pragma unroll
-        for (int j = 0; j < SEL_KPT; ++j)
+        for (int j = 0; j < KPT; ++j)
             if ((ma >> j) & 1u) out[rank[j]] = i0 + j;
     }
+}
+
+template <bool SORTED>
+__device__ __attribute__((always_inline)) void select_row(const float* srow, int P, int n1, int n2,
+                                                          int32_t* out, SelectSmem& sm,
+                                                          uint32_t* skeys) {
+    const int kpt = (P + SEL_THREADS - 1) / SEL_THREADS;
+    if (kpt <= 1)
+        select_row_k<SORTED, 1>(srow, P, n1, n2, out, sm, skeys);
+    else if (kpt <= 2)
+        select_row_k<SORTED, 2>(srow, P, n1, n2, out, sm, skeys);
+    else if (kpt <= 4)
+        select_row_k<SORTED, 4>(srow, P, n1, n2, out, sm, skeys);
+    else if (kpt <= 8)
+        select_row_k<SORTED, 8>(srow, P, n1, n2, out, sm, skeys);
+    else if (kpt <= 16)
+        select_row_k<SORTED, 16>(srow, P, n1, n2, out, sm, skeys);
+    else
+        select_row_k<SORTED, 32>(srow, P, n1, n2, out, sm, skeys);
 }
 
 template <bool FUSED>
