@@ -27,7 +27,9 @@
 //    lane-partial until the end.  Rescaling the 32 accumulator registers is
 //    skipped when no row's max moved (wave-uniform branch).
 //  * INT8: K codes become exact fp16 (byte splice, i8x4_to_h4) and K's
-//    per-channel scale is folded into the query operand per page; V's
+//    per-channel scale is folded into the query operand per page (the
+//    512-byte scale row is loaded 8 bytes a lane and handed to the 16 lanes
+//    that use each channel through a per-wave LDS slot); V's
 //    per-token scale is folded into the softmax weights (as the reference
 //    does, paged_decode_int8.cu:230-242).  The sequence's last page takes K
 //    from the fp16 residual (paged_decode.py:213-216).
@@ -51,7 +53,7 @@ namespace ls {
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 
-template <int NWT, int HG>
+template <int NWT, int HG, bool SCALES>
 struct DecodeSmem {
     // During the walk the merge buffer holds the group's item table: the
     // block of every page of its range (dense walk, shared by the heads) or,
@@ -64,6 +66,8 @@ struct DecodeSmem {
     static constexpr int ENT_INTS = 2048 * HG;
     float m[HG][NWT][MAX_NREP];
     float l[HG][NWT][MAX_NREP];
+    // INT8: each wave's K scale (and zero point) row of the page it computes
+    float kscale[SCALES ? NWT : 1][2][HEAD_DIM];
     float acc[HG][NWT][MAX_NREP][ROW];
     int ent[ENT_INTS];
     int is_last[HG];
@@ -75,8 +79,8 @@ struct DecodeSmem {
 struct PageBuf {
     u4 k[4];      // K row `c`, channels 32j+8g..+8   (fp16: 16 B, int8: 8 B)
     u4 v[4];      // V row 4g+i, channels 8c..8c+8     (fp16: 16 B, int8: 8 B)
-    f4 ks[4][2];  // INT8: K scale of the same channels (32 B per j)
-    f4 kz[4][2];  // INT8 asym: K zero points
+    u2 ks;        // INT8: K scales of channels 2*lane, 2*lane+1 (the row is 512 B)
+    u2 kz;        // INT8 asym: K zero points, as ks
     float vs[4];  // INT8: V scale of tokens 4g+i
     float vz[4];  // INT8 asym: V zero points
     int res;      // INT8: this page's K comes from the residual
@@ -125,19 +129,15 @@ __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, i
                 buf.k[j].x = t.x;
                 buf.k[j].y = t.y;
             }
-            const float* ksp = a.k_scale + (int64_t)blk * a.sks_b + (int64_t)h * a.sks_h + 8 * g;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                buf.ks[j][0] = *(const f4*)(ksp + 32 * j);
-                buf.ks[j][1] = *(const f4*)(ksp + 32 * j + 4);
-            }
+            // One coalesced 512-byte row per page, 8 bytes a lane; the
+            // compute step spreads it through LDS to the lanes that need
+            // each channel (16 lanes share every scale).
+            const int lane = 16 * g + c;
+            const float* ksp = a.k_scale + (int64_t)blk * a.sks_b + (int64_t)h * a.sks_h;
+            buf.ks = *(const u2*)(ksp + 2 * lane);
             if (ASYM) {
-                const float* kzp = a.k_zero + (int64_t)blk * a.sks_b + (int64_t)h * a.sks_h + 8 * g;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    buf.kz[j][0] = *(const f4*)(kzp + 32 * j);
-                    buf.kz[j][1] = *(const f4*)(kzp + 32 * j + 4);
-                }
+                const float* kzp = a.k_zero + (int64_t)blk * a.sks_b + (int64_t)h * a.sks_h;
+                buf.kz = *(const u2*)(kzp + 2 * lane);
             }
         }
     }
@@ -152,8 +152,8 @@ struct WaveState {
 
 template <int KIND, bool ASYM>
 __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, const h4 (&qh)[8],
-                                             const float (&qf)[4][8], int page, int len,
-                                             float scale_log2, int g) {
+                                             int page, int len, float scale_log2, int g,
+                                             float (*kscale)[HEAD_DIM]) {
     // ---- S^T = K . Q^T ----
     f4 s = {0.f, 0.f, 0.f, 0.f};
     float qz = 0.f;
@@ -172,16 +172,31 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
                 s = mfma16(as_h4(buf.k[j].z, buf.k[j].w), qh[2 * j + 1], s);
             }
         } else {
+            // the wave's scale row through LDS (one wave's accesses stay in
+            // order, so each read sees this page's row)
+            const int lane = __lane_id();
+            *(u2*)&kscale[0][2 * lane] = buf.ks;
+            if (ASYM) *(u2*)&kscale[1][2 * lane] = buf.kz;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const u2 lo = i8x4_to_h4(buf.k[j].x);
                 const u2 hi = i8x4_to_h4(buf.k[j].y);
+                const f4 ks0 = *(const f4*)&kscale[0][32 * j + 8 * g];
+                const f4 ks1 = *(const f4*)&kscale[0][32 * j + 8 * g + 4];
+                f4 kz0 = {0.f, 0.f, 0.f, 0.f}, kz1 = {0.f, 0.f, 0.f, 0.f};
+                if (ASYM) {
+                    kz0 = *(const f4*)&kscale[1][32 * j + 8 * g];
+                    kz1 = *(const f4*)&kscale[1][32 * j + 8 * g + 4];
+                }
+                // q (fp16) x scale (fp32) rounded once to fp16: mixed-precision
+                // multiplies straight from the fp16 query registers
                 h4 q0, q1;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    q0[e] = (half_t)(qf[j][e] * buf.ks[j][0][e]);
-                    q1[e] = (half_t)(qf[j][4 + e] * buf.ks[j][1][e]);
-                    if (ASYM) qz += qf[j][e] * buf.kz[j][0][e] + qf[j][4 + e] * buf.kz[j][1][e];
+                    const float qa = (float)qh[2 * j][e], qb = (float)qh[2 * j + 1][e];
+                    q0[e] = (half_t)(qa * ks0[e]);
+                    q1[e] = (half_t)(qb * ks1[e]);
+                    if (ASYM) qz += qa * kz0[e] + qb * kz1[e];
                 }
                 s = mfma16(as_h4(lo.x, lo.y), q0, s);
                 s = mfma16(as_h4(hi.x, hi.y), q1, s);
@@ -360,11 +375,12 @@ __device__ __forceinline__ int claimed_item(int raw) { return __builtin_amdgcn_r
 
 template <int KIND, bool ASYM, bool HAS_RES, bool SPARSE, int NWT, int HG, int ABL = 0>
 __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodeParams a) {
-    // Pages in flight ahead of the one being computed: the fp16 page buffer
-    // is 32 VGPRs, the INT8 one (codes + K scales) as large again.
+    // Pages in flight ahead of the one being computed.  INT8 keeps one: a
+    // second buffer would take its kernels past 256 registers, to one wave
+    // per SIMD.
     constexpr int PF_DEPTH = KIND == KV_FP16 ? 2 : 1;
     constexpr int NB = PF_DEPTH + 1;
-    __shared__ DecodeSmem<NWT, HG> sm;
+    __shared__ DecodeSmem<NWT, HG, KIND == KV_INT8> sm;
     const int H = a.H;
     // A group serves HG adjacent KV heads of one (sequence, split) with NWT
     // waves.  Its work items are (page, head) pairs, claimed one at a time
@@ -440,7 +456,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // entries outside the sequence and a last page whose residual row is
     // outside the residual become -1 and are never dereferenced.  A range
     // longer than the table resolves each claimed item from global memory.
-    constexpr int ENT_INTS = DecodeSmem<NWT, HG>::ENT_INTS;
+    constexpr int ENT_INTS = DecodeSmem<NWT, HG, KIND == KV_INT8>::ENT_INTS;
     constexpr int CAP = SPARSE ? ENT_INTS / (2 * HG) : ENT_INTS;
     const bool cached = n_ent <= CAP;
     auto resolve_global = [&](int e, int hh, int& blk, int& pg) {
@@ -482,7 +498,6 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // Query operands of the group's heads: row c (zero beyond n_rep),
     // channels 32j+8g..+8.
     h4 qh[HG][8];
-    float qf[HG][4][8];
 #pragma unroll
     for (int hh = 0; hh < HG; ++hh) {
         const bool row_ok = c < a.NR;
@@ -494,11 +509,6 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             if (row_ok) t = *(const u4*)(qp + 32 * j);
             qh[hh][2 * j] = as_h4(t.x, t.y);
             qh[hh][2 * j + 1] = as_h4(t.z, t.w);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                qf[hh][j][e] = (float)qh[hh][2 * j][e];
-                qf[hh][j][4 + e] = (float)qh[hh][2 * j + 1][e];
-            }
         }
     }
     const float scale_log2 = a.scale * LOG2E;
@@ -605,8 +615,8 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                         if (ABL == 1 || ABL == 2)
                             consume_page(buf[u], st[hh]);
                         else
-                            compute_page<KIND, ASYM>(buf[u], st[hh], qh[hh], qf[hh], pgs[u],
-                                                     live_len, scale_log2, g);
+                            compute_page<KIND, ASYM>(buf[u], st[hh], qh[hh], pgs[u],
+                                                     live_len, scale_log2, g, sm.kscale[wv]);
                     }
                 }
                 // items arrive in increasing order: past the end, all later are too
