@@ -58,7 +58,7 @@ enum {
 /* Message for the last non-zero return on this thread. */
 const char* ls_last_error(void);
 
-/* ABI version (bumped on any signature change). */
+/* ABI version (bumped on any signature change or addition). */
 int ls_abi_version(void);
 
 /* Bytes of `workspace` a decode call with these sizes needs (0 when
@@ -183,6 +183,43 @@ int ls_page_bounds_update(const void* k_new, const int64_t* kn_strides, const in
 int ls_page_bounds_rebuild(const void* k_pool, const int64_t* kv_strides, int num_blocks,
                            void* kmin, void* kmax, const int64_t* bound_strides, int kv_heads,
                            int head_dim, int page, void* stream);
+
+/* ---- INT8 cache write side ------------------------------------------- *
+ * Quantizer constants as the reference cache holds them (k_bits / v_bits
+ * = 8: qmax 127, levels 255, offset 128; eps 1e-8).  recip = 1 divides by
+ * qmax / levels as a multiply by the fp32 reciprocal formed on the host
+ * (torch's `t / python_number` on a GPU, and the reference's int8_write.cu);
+ * recip = 0 divides exactly (torch on the CPU).  Either way the codes and
+ * scales are bit-exact with that form of the reference's torch ops.
+ */
+
+/* Decode-step write for one token per sequence: V [B, H_kv, 128] fp16
+ * (v_strides[2] = (b, h)) quantized per (token, head) into flat_v int8
+ * [num_slots, H_kv, 128] / flat_v_scale (and flat_v_zero when asym) fp32
+ * [num_slots, H_kv] at row slots[b]; K [B, H_kv, 128] copied into the fp16
+ * residual k_res [num_res, H_kv, 128] at row res_idx[b].  slots / res_idx
+ * int64; rows outside [0, num_slots) / [0, num_res) are skipped.  Replaces
+ * int8_decode_write (kernels/cuda/int8_write.cu:46-80; decode_write,
+ * kernels/cuda/int8_write.py:61-82). */
+int ls_int8_decode_write(const void* k, const int64_t* k_strides, const void* v,
+                         const int64_t* v_strides, const int64_t* slots, const int64_t* res_idx,
+                         void* flat_v, float* flat_v_scale, float* flat_v_zero, void* k_res,
+                         int64_t num_slots, int64_t num_res, int batch, int kv_heads,
+                         int head_dim, int asym, float eps, float qmax, float levels,
+                         float offset, int recip, void* stream);
+
+/* K quantizer of completed pages: data fp16 [n, 16, H_kv, 128]
+ * (data_strides[3] = (block, token, head)) -> int8 codes into k_pool block
+ * ids[n] (kv_strides[3]), step into k_scale [num_blocks, H_kv, 128]
+ * (ks_strides[2] = (block, head)), zero point into k_zero (asym), one step per
+ * (block, head, channel) over the 16 tokens.  ids int64; ids outside the
+ * pool are skipped.  Replaces Int8PagedKVCache._finalize_blocks
+ * (cache/int8_paged_cache.py:670-699). */
+int ls_int8_finalize_blocks(const void* data, const int64_t* data_strides, const int64_t* ids,
+                            int n, void* k_pool, const int64_t* kv_strides, float* k_scale,
+                            float* k_zero, const int64_t* ks_strides, int64_t num_blocks,
+                            int kv_heads, int head_dim, int page, int asym, float eps, float qmax,
+                            float levels, float offset, int recip, void* stream);
 
 #ifdef __cplusplus
 }

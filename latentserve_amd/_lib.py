@@ -24,6 +24,9 @@ _I64 = ctypes.c_int64
 
 LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
+# The ABI this binding is written for (include/latentserve_amd.h); a library
+# built from other sources is refused rather than called with wrong arguments.
+ABI_VERSION = 4
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -53,6 +56,12 @@ _SIGNATURES = {
         _VP, _I64P, _VP, _VP, _VP, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
     "ls_page_bounds_rebuild": [
         _VP, _I64P, _I32, _VP, _VP, _I64P, _I32, _I32, _I32, _VP],
+    "ls_int8_decode_write": [
+        _VP, _I64P, _VP, _I64P, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I32, _I32, _I32,
+        _I32, _F32, _F32, _F32, _F32, _I32, _VP],
+    "ls_int8_finalize_blocks": [
+        _VP, _I64P, _VP, _I32, _VP, _I64P, _VP, _VP, _I64P, _I64, _I32, _I32, _I32, _I32,
+        _F32, _F32, _F32, _F32, _I32, _VP],
     "ls_combine_splits": [
         _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
 }
@@ -82,6 +91,11 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = argtypes
             fn.restype = {"ls_last_error": ctypes.c_char_p,
                           "ls_decode_workspace_bytes": ctypes.c_size_t}.get(name, ctypes.c_int)
+        got = handle.ls_abi_version()
+        if got != ABI_VERSION:
+            raise HipLibraryMissing(
+                f"{LIB_PATH} has ABI {got}, this binding expects {ABI_VERSION}: rebuild it with "
+                "`python -m latentserve_amd.csrc.build`")
         _lib = handle
     return _lib
 

@@ -19,7 +19,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 LIB = os.path.join(PKG, "liblatentserve_hip.so")
-SOURCES = ["ls_abi.hip", "ls_decode.hip", "ls_sparse_index.hip"]
+SOURCES = ["ls_abi.hip", "ls_decode.hip", "ls_sparse_index.hip", "ls_int8_write.hip"]
 ARCH = os.environ.get("LS_OFFLOAD_ARCH", "gfx950")
 
 # Packed-fp32 VALU forms are disabled for every device pass; fp32 division
@@ -27,7 +27,8 @@ ARCH = os.environ.get("LS_OFFLOAD_ARCH", "gfx950")
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-fno-fast-math", "-Wall", "-Wno-unused-function",
+    "-fno-fast-math", "-fhip-fp32-correctly-rounded-divide-sqrt", "-Wall",
+    "-Wno-unused-function",
 ]
 
 

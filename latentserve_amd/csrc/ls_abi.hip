@@ -18,6 +18,7 @@
 #include "ls_common.h"
 #include "ls_decode.h"
 #include "ls_sparse.h"
+#include "ls_int8_write.h"
 
 namespace {
 
@@ -128,7 +129,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 3; }
+int ls_abi_version(void) { return 4; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -444,6 +445,101 @@ int ls_page_bounds_rebuild(const void* k_pool, const int64_t* kv_strides, int nu
     a.B = 0;
     a.H = kv_heads;
     return hip_status(ls::launch_bounds_rebuild(a, (hipStream_t)stream), "ls_page_bounds_rebuild");
+}
+
+static int quant_args(int asym, float eps, float qmax, float levels, float offset, int recip,
+                      ls::QuantArgs& q) {
+    if (!(qmax >= 1.f && qmax <= 127.f) || !(levels >= 1.f && levels <= 255.f) ||
+        !(offset >= 0.f && offset <= 128.f) || !(eps >= 0.f))
+        return fail(LS_ERR_INVALID, "bad quantizer constants (qmax %g, levels %g, offset %g, eps %g)",
+                    qmax, levels, offset, eps);
+    q.asym = asym ? 1 : 0;
+    q.recip = recip ? 1 : 0;
+    q.eps = eps;
+    q.qmax = qmax;
+    q.levels = levels;
+    q.offset = offset;
+    // the reciprocal as torch forms it for `t / python_number` on a GPU:
+    // one fp32 division on the host
+    volatile float one = 1.0f;
+    q.inv_qmax = one / qmax;
+    q.inv_levels = one / levels;
+    return LS_OK;
+}
+
+int ls_int8_decode_write(const void* k, const int64_t* k_strides, const void* v,
+                         const int64_t* v_strides, const int64_t* slots, const int64_t* res_idx,
+                         void* flat_v, float* flat_v_scale, float* flat_v_zero, void* k_res,
+                         int64_t num_slots, int64_t num_res, int batch, int kv_heads,
+                         int head_dim, int asym, float eps, float qmax, float levels,
+                         float offset, int recip, void* stream) {
+    if (!k || !k_strides || !v || !v_strides || !slots || !res_idx || !flat_v || !flat_v_scale ||
+        !k_res)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (asym && !flat_v_zero) return fail(LS_ERR_INVALID, "asymmetric quantization needs flat_v_zero");
+    if (head_dim != ls::HEAD_DIM) return fail(LS_ERR_INVALID, "head_dim must be 128, got %d", head_dim);
+    if (batch < 0 || kv_heads < 1 || num_slots < 0 || num_res < 0)
+        return fail(LS_ERR_INVALID, "bad batch, kv_heads, num_slots or num_res");
+    if (!rows_aligned(k, k_strides, 2, 2, 4) || !rows_aligned(v, v_strides, 2, 2, 4) ||
+        !aligned(flat_v, 2) || !aligned(k_res, 4) || !aligned(flat_v_scale, 4))
+        return fail(LS_ERR_INVALID, "k, v, flat_v and k_res rows must be aligned to channel pairs");
+    ls::DecodeWriteParams a;
+    if (int rc = quant_args(asym, eps, qmax, levels, offset, recip, a.q)) return rc;
+    if (batch == 0) return LS_OK;
+    a.k = k;
+    a.sk_b = k_strides[0];
+    a.sk_h = k_strides[1];
+    a.v = v;
+    a.sv_b = v_strides[0];
+    a.sv_h = v_strides[1];
+    a.slots = slots;
+    a.res_idx = res_idx;
+    a.flat_v = flat_v;
+    a.flat_v_scale = flat_v_scale;
+    a.flat_v_zero = flat_v_zero;
+    a.k_res = k_res;
+    a.num_slots = num_slots;
+    a.num_res = num_res;
+    a.B = batch;
+    a.H = kv_heads;
+    return hip_status(ls::launch_decode_write(a, (hipStream_t)stream), "ls_int8_decode_write");
+}
+
+int ls_int8_finalize_blocks(const void* data, const int64_t* data_strides, const int64_t* ids,
+                            int n, void* k_pool, const int64_t* kv_strides, float* k_scale,
+                            float* k_zero, const int64_t* ks_strides, int64_t num_blocks,
+                            int kv_heads, int head_dim, int page, int asym, float eps, float qmax,
+                            float levels, float offset, int recip, void* stream) {
+    if (!data || !data_strides || !ids || !k_pool || !kv_strides || !k_scale || !ks_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (asym && !k_zero) return fail(LS_ERR_INVALID, "asymmetric quantization needs k_zero");
+    if (head_dim != ls::HEAD_DIM) return fail(LS_ERR_INVALID, "head_dim must be 128, got %d", head_dim);
+    if (page != ls::PAGE) return fail(LS_ERR_INVALID, "page (block_size) must be 16, got %d", page);
+    if (n < 0 || kv_heads < 1 || num_blocks < 0)
+        return fail(LS_ERR_INVALID, "bad n, kv_heads or num_blocks");
+    if (!rows_aligned(data, data_strides, 3, 2, 4) || !rows_aligned(k_pool, kv_strides, 3, 1, 2) ||
+        !aligned(k_scale, 4))
+        return fail(LS_ERR_INVALID, "data, k_pool and k_scale rows must be aligned to channel pairs");
+    ls::FinalizeParams a;
+    if (int rc = quant_args(asym, eps, qmax, levels, offset, recip, a.q)) return rc;
+    if (n == 0) return LS_OK;
+    a.data = data;
+    a.sd_n = data_strides[0];
+    a.sd_t = data_strides[1];
+    a.sd_h = data_strides[2];
+    a.ids = ids;
+    a.k_pool = k_pool;
+    a.sp_b = kv_strides[0];
+    a.sp_t = kv_strides[1];
+    a.sp_h = kv_strides[2];
+    a.k_scale = k_scale;
+    a.k_zero = k_zero;
+    a.ss_b = ks_strides[0];
+    a.ss_h = ks_strides[1];
+    a.num_blocks = num_blocks;
+    a.N = n;
+    a.H = kv_heads;
+    return hip_status(ls::launch_finalize_k(a, (hipStream_t)stream), "ls_int8_finalize_blocks");
 }
 
 }  // extern "C"

@@ -207,8 +207,9 @@ def combine(partial_acc, partial_m, partial_l) -> np.ndarray:
     return out
 
 
-def quantize_k(data, asym: bool = False, eps: float = 1e-8, bits: int = 8):
-    """``_finalize_blocks`` (cache/int8_paged_cache.py:670-699).
+def quantize_k(data, asym: bool = False, eps: float = 1e-8, bits: int = 8, recip: bool = False):
+    """``_finalize_blocks`` (cache/int8_paged_cache.py:670-699).  recip: divide
+    by qmax / levels as torch does on a GPU (times the fp32 reciprocal).
 
     data fp16 [N, PAGE, H, D] -> (codes int8 [N, PAGE, H, D], step fp32 [N, H, D],
     zero fp32 [N, H, D] or None).
@@ -220,12 +221,14 @@ def quantize_k(data, asym: bool = False, eps: float = 1e-8, bits: int = 8):
     zero = np.empty((n, h, d), dtype=np.float32) if asym else None
     lib().ls_ref_quantize_k(_ptr(data), _I32(n), _I32(page), _I32(h), _I32(d), _I32(int(asym)),
                             _F32(eps), _F32(2 ** (bits - 1) - 1), _F32(2 ** bits - 1),
-                            _F32(2 ** (bits - 1)), _ptr(codes), _ptr(step), _ptr(zero))
+                            _F32(2 ** (bits - 1)), _I32(int(recip)), _ptr(codes), _ptr(step),
+                            _ptr(zero))
     return codes, step, zero
 
 
-def quantize_v(v, asym: bool = False, eps: float = 1e-8, bits: int = 8):
-    """V's per-token quantizer (cache/int8_paged_cache.py:741-758).
+def quantize_v(v, asym: bool = False, eps: float = 1e-8, bits: int = 8, recip: bool = False):
+    """V's per-token quantizer (cache/int8_paged_cache.py:741-758); recip as
+    for quantize_k.
 
     v fp16 [..., H, D] -> (codes int8 same shape, step fp32 [..., H], zero or None).
     """
@@ -238,7 +241,8 @@ def quantize_v(v, asym: bool = False, eps: float = 1e-8, bits: int = 8):
     zero = np.empty(lead + (h,), dtype=np.float32) if asym else None
     lib().ls_ref_quantize_v(_ptr(v), _I32(t), _I32(h), _I32(d), _I32(int(asym)), _F32(eps),
                             _F32(2 ** (bits - 1) - 1), _F32(2 ** bits - 1),
-                            _F32(2 ** (bits - 1)), _ptr(codes), _ptr(step), _ptr(zero))
+                            _F32(2 ** (bits - 1)), _I32(int(recip)), _ptr(codes), _ptr(step),
+                            _ptr(zero))
     return codes, step, zero
 
 

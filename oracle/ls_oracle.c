@@ -27,9 +27,12 @@
  *                          cache/block_allocator.py:214-220 (slot rule).
  *
  * Arithmetic is fp32 with no contraction (build with -ffp-contract=off) so a
- * multiply followed by an add rounds twice, as the torch CPU ops do.  Integer
- * codes use IEEE division and round-half-to-even (rintf), which is what torch
- * CPU's `t / python_number` and `torch.round` compute.
+ * multiply followed by an add rounds twice, as the torch ops do.  Integer
+ * codes use round-half-to-even (rintf, torch.round).  The quantizers take
+ * `recip`: torch divides a tensor by a Python number as an IEEE division on
+ * the CPU (recip = 0) and as a multiply by the fp32 reciprocal formed on the
+ * host on a GPU (recip = 1, also what kernels/cuda/int8_write.cu:20-24, 62-73
+ * computes); tensor-by-tensor divisions are IEEE divisions either way.
  *
  * fp16 values cross this boundary as raw uint16 bit patterns.  Strides are in
  * elements.  All (b, head) pairs are independent and are spread over OpenMP
@@ -342,8 +345,9 @@ void ls_ref_combine(int B, int H, int S, int NR, int D, const float* acc, const 
  * Asymmetric: step = max((hi - lo) / levels, eps); u = clamp(rint((f - lo)/step), 0, levels);
  * q = u - offset; zero = lo + offset * step. */
 void ls_ref_quantize_k(const uint16_t* data, int N, int PAGE, int H, int D, int asym, float eps,
-                       float qmax, float levels, float offset, int8_t* codes, float* step,
-                       float* zero) {
+                       float qmax, float levels, float offset, int recip, int8_t* codes,
+                       float* step, float* zero) {
+    const float inv_qmax = 1.0f / qmax, inv_levels = 1.0f / levels;
 #pragma omp parallel for schedule(static)
     for (int64_t nh = 0; nh < (int64_t)N * H; ++nh) {
         const int64_t n = nh / H;
@@ -360,11 +364,12 @@ void ls_ref_quantize_k(const uint16_t* data, int N, int PAGE, int H, int D, int 
             }
             float s;
             if (asym) {
-                s = (hi - lo) / levels;
+                s = recip ? (hi - lo) * inv_levels : (hi - lo) / levels;
                 if (s < eps) s = eps;
                 zero[sidx] = lo + offset * s;
             } else {
-                s = (amax < eps ? eps : amax) / qmax;
+                const float m = amax < eps ? eps : amax;
+                s = recip ? m * inv_qmax : m / qmax;
             }
             step[sidx] = s;
             for (int t = 0; t < PAGE; ++t) {
@@ -388,7 +393,9 @@ void ls_ref_quantize_k(const uint16_t* data, int N, int PAGE, int H, int D, int 
 /* V's per-token quantizer (cache/int8_paged_cache.py:741-758).
  * v fp16 [T, H, D] contiguous -> codes int8 [T, H, D], step/zero fp32 [T, H]. */
 void ls_ref_quantize_v(const uint16_t* v, int T, int H, int D, int asym, float eps, float qmax,
-                       float levels, float offset, int8_t* codes, float* step, float* zero) {
+                       float levels, float offset, int recip, int8_t* codes, float* step,
+                       float* zero) {
+    const float inv_qmax = 1.0f / qmax, inv_levels = 1.0f / levels;
 #pragma omp parallel for schedule(static)
     for (int64_t th = 0; th < (int64_t)T * H; ++th) {
         const uint16_t* row = v + th * D;
@@ -402,11 +409,12 @@ void ls_ref_quantize_v(const uint16_t* v, int T, int H, int D, int asym, float e
         }
         float s;
         if (asym) {
-            s = (hi - lo) / levels;
+            s = recip ? (hi - lo) * inv_levels : (hi - lo) / levels;
             if (s < eps) s = eps;
             zero[th] = lo + offset * s;
         } else {
-            s = (amax < eps ? eps : amax) / qmax;
+            const float m = amax < eps ? eps : amax;
+            s = recip ? m * inv_qmax : m / qmax;
         }
         step[th] = s;
         for (int d = 0; d < D; ++d) {
