@@ -221,6 +221,19 @@ int ls_int8_finalize_blocks(const void* data, const int64_t* data_strides, const
                             int kv_heads, int head_dim, int page, int asym, float eps, float qmax,
                             float levels, float offset, int recip, void* stream);
 
+/* Block-table gather (the paged cache's read path): out [B, length, H_kv,
+ * head_dim] (out_strides[3] = (b, token, head)) gets, for token p of
+ * sequence b, the pool row of flat slot table[b][p / 16] * 16 + p % 16 when
+ * p < seq_lens[b], else flat slot 0 (the reference's zero-padded slot
+ * table).  pool [num_blocks, 16, H_kv, head_dim] of elem_bytes-byte elements
+ * (fp16 2, int8 1, fp32 4).  Bit-exact byte copy.  Replaces read()
+ * (cache/paged_cache.py:486-506, slot table :305-323; slot rule
+ * cache/block_allocator.py:214-220). */
+int ls_paged_gather(const void* pool, int elem_bytes, const int64_t* kv_strides, int num_blocks,
+                    const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                    const int32_t* seq_lens, void* out, const int64_t* out_strides, int batch,
+                    int kv_heads, int head_dim, int page, int length, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,7 +26,7 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -62,6 +62,9 @@ _SIGNATURES = {
     "ls_int8_finalize_blocks": [
         _VP, _I64P, _VP, _I32, _VP, _I64P, _VP, _VP, _I64P, _I64, _I32, _I32, _I32, _I32,
         _F32, _F32, _F32, _F32, _I32, _VP],
+    "ls_paged_gather": [
+        _VP, _I32, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P, _I32, _I32, _I32, _I32, _I32,
+        _VP],
     "ls_combine_splits": [
         _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
 }

@@ -19,6 +19,7 @@
 #include "ls_decode.h"
 #include "ls_sparse.h"
 #include "ls_int8_write.h"
+#include "ls_gather.h"
 
 namespace {
 
@@ -129,7 +130,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 4; }
+int ls_abi_version(void) { return 5; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -540,6 +541,49 @@ int ls_int8_finalize_blocks(const void* data, const int64_t* data_strides, const
     a.N = n;
     a.H = kv_heads;
     return hip_status(ls::launch_finalize_k(a, (hipStream_t)stream), "ls_int8_finalize_blocks");
+}
+
+int ls_paged_gather(const void* pool, int elem_bytes, const int64_t* kv_strides, int num_blocks,
+                    const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                    const int32_t* seq_lens, void* out, const int64_t* out_strides, int batch,
+                    int kv_heads, int head_dim, int page, int length, void* stream) {
+    if (!pool || !kv_strides || !block_tables || !seq_lens || !out || !out_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4)
+        return fail(LS_ERR_INVALID, "elem_bytes must be 1, 2 or 4, got %d", elem_bytes);
+    if (page != ls::PAGE) return fail(LS_ERR_INVALID, "page (block_size) must be 16, got %d", page);
+    if (head_dim < 1 || (head_dim * elem_bytes) % 16 != 0)
+        return fail(LS_ERR_INVALID, "a head row must be a multiple of 16 bytes (head_dim %d)",
+                    head_dim);
+    if (batch < 0 || batch > 65535 || kv_heads < 1 || length < 0 || max_pages < 0 ||
+        num_blocks < 1)
+        return fail(LS_ERR_INVALID, "bad batch, kv_heads, length, max_pages or num_blocks");
+    if ((int64_t)length * kv_heads * (head_dim * elem_bytes / 16) > (1LL << 31) - 256)
+        return fail(LS_ERR_INVALID, "length x heads too large for one gather");
+    if (!rows_aligned(pool, kv_strides, 3, (size_t)elem_bytes, 16) ||
+        !rows_aligned(out, out_strides, 3, (size_t)elem_bytes, 16))
+        return fail(LS_ERR_INVALID, "pool and out rows must be 16-byte aligned");
+    if (batch == 0 || length == 0) return LS_OK;
+    ls::GatherParams a;
+    a.pool = pool;
+    a.sp_b = kv_strides[0];
+    a.sp_t = kv_strides[1];
+    a.sp_h = kv_strides[2];
+    a.num_blocks = num_blocks;
+    a.block_tables = block_tables;
+    a.sbt_b = bt_stride;
+    a.max_pages = max_pages;
+    a.seq_lens = seq_lens;
+    a.out = out;
+    a.so_b = out_strides[0];
+    a.so_t = out_strides[1];
+    a.so_h = out_strides[2];
+    a.elem = elem_bytes;
+    a.row_bytes = head_dim * elem_bytes;
+    a.B = batch;
+    a.L = length;
+    a.H = kv_heads;
+    return hip_status(ls::launch_gather(a, (hipStream_t)stream), "ls_paged_gather");
 }
 
 }  // extern "C"

@@ -291,7 +291,9 @@ def bounds_update(k_new, slots, kmin, kmax, page: int = 16) -> None:
 
 
 def gather(pool, block_tables, seq_lens, lmax: int):
-    """The gather read (cache/paged_cache.py:486-506): [B, H, lmax, D], zero past each length."""
+    """The gather read (cache/paged_cache.py:486-506): [B, H, lmax, D]; positions
+    past a sequence's length hold flat slot 0, as the reference's padded slot
+    table reads (:305-323)."""
     pool = np.ascontiguousarray(pool)
     nb, page, h, d = pool.shape
     b = block_tables.shape[0]

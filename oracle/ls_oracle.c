@@ -500,18 +500,21 @@ void ls_ref_bounds_update(const uint16_t* k_new, const int64_t* slots, int B, in
 
 /* ------------------------------------------------------------ gather ---- */
 
-/* The gather read path: token p of sequence b lives at flat slot
- * blocks[p / PAGE] * PAGE + p % PAGE.  pool [nb, PAGE, H, D] of `elem`-byte
- * elements, contiguous; out [B, H, Lmax, D] contiguous, rows past a sequence's
- * length left untouched. */
+/* The gather read path (cache/paged_cache.py:486-506 with _build_read_slots,
+ * :305-323): token p < L of sequence b lives at flat slot
+ * blocks[p / PAGE] * PAGE + p % PAGE; positions past a sequence's length
+ * read flat slot 0 (the reference pads its slot table with 0 and leaves the
+ * masking to the caller).  pool [nb, PAGE, H, D] of `elem`-byte elements,
+ * contiguous; out [B, H, Lmax, D] contiguous. */
 void ls_ref_gather(const void* pool, int elem, const int32_t* block_tables, int64_t sbt_b,
                    const int32_t* seq_lens, int B, int H, int D, int PAGE, int Lmax, void* out) {
     const char* src = (const char*)pool;
     char* dst = (char*)out;
     for (int b = 0; b < B; ++b) {
-        const int L = seq_lens[b] < Lmax ? seq_lens[b] : Lmax;
-        for (int p = 0; p < L; ++p) {
-            const int64_t slot = (int64_t)block_tables[(int64_t)b * sbt_b + p / PAGE] * PAGE + p % PAGE;
+        const int L = seq_lens[b];
+        for (int p = 0; p < Lmax; ++p) {
+            const int64_t slot =
+                p < L ? (int64_t)block_tables[(int64_t)b * sbt_b + p / PAGE] * PAGE + p % PAGE : 0;
             for (int h = 0; h < H; ++h)
                 memcpy(dst + ((((int64_t)b * H + h) * Lmax + p) * D) * elem,
                        src + ((slot * H + h) * D) * elem, (size_t)D * elem);

@@ -400,4 +400,6 @@ def test_gather_follows_the_slot_rule():
         for p in range(L):
             slot = int(t[b, p // 16]) * 16 + p % 16
             np.testing.assert_array_equal(g[b, :, p], k.reshape(-1, 2, 128)[slot])
-        assert (g[b, :, L:] == 0).all()
+        # past the length: flat slot 0 (the reference pads its slot table with 0)
+        np.testing.assert_array_equal(g[b, :, L:], np.broadcast_to(
+            k.reshape(-1, 2, 128)[0][:, None], (2, 48 - L, 128)))
