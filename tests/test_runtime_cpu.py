@@ -1,0 +1,99 @@
+"""Cache bookkeeping on the CPU: allocator, block tables, advance / write.
+
+Follows the reference's own cache tests (tests/test_phase3_paged_cache.py:
+LIFO reuse, the slot rule, out-of-blocks as a typed error; capacity-width
+persistent tables, tests/test_phase13_graph.py)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from latentserve_amd.runtime.kv_cache import (BlockAllocator, BlockTable, KVCacheSpec,
+                                              OutOfBlocks, PagedKVCache)
+
+
+def test_allocator_hands_out_ascending_then_reuses_lifo():
+    a = BlockAllocator(num_blocks=8, block_size=16)
+    assert a.allocate(3) == [0, 1, 2]
+    a.free([1])
+    a.free([0])
+    assert a.allocate(2) == [0, 1]          # most recently freed first
+    assert a.num_used == 3 and a.peak_used == 3
+
+
+def test_allocator_out_of_blocks_is_typed_and_refcounts_hold():
+    a = BlockAllocator(num_blocks=2, block_size=16)
+    blocks = a.allocate(2)
+    with pytest.raises(OutOfBlocks):
+        a.allocate(1)
+    a.incref([blocks[0]])
+    a.free(blocks)
+    assert a.num_free == 1                  # block 0 still referenced once
+    with pytest.raises(ValueError):
+        a.free([blocks[1]])
+
+
+def test_block_table_slot_rule():
+    a = BlockAllocator(num_blocks=10, block_size=16)
+    a.allocate(3)                           # make the table's blocks non-trivial
+    t = BlockTable(a)
+    t.append(40)
+    assert t.blocks == [3, 4, 5]
+    assert t.slot(0) == 48 and t.slot(17) == 4 * 16 + 1 and t.slot(39) == 5 * 16 + 7
+    with pytest.raises(IndexError):
+        t.slot(40)
+    v = t.version
+    t.append(8)                             # still inside block 5: no new block
+    assert t.version == v and len(t.blocks) == 3
+    t.append(1)
+    assert t.version == v + 1 and len(t.blocks) == 4
+
+
+def _cache(batch=3, cap=100, layers=2):
+    spec = KVCacheSpec(num_layers=layers, num_kv_heads=2, head_dim=128, max_batch_size=batch,
+                       max_seq_len=cap, device="cpu")
+    return PagedKVCache(spec)
+
+
+def test_advance_keeps_persistent_capacity_width_buffers():
+    c = _cache()
+    c.advance(20, batch_size=2)
+    bt, sl = c.block_tables_tensor(), c.seq_lens_tensor()
+    base = c._block_tables_buf.data_ptr()
+    assert bt.shape == (2, 7) and sl.tolist() == [20, 20]
+    assert bt.data_ptr() == base
+    c.advance(1, slots=[1, 0])
+    assert c.seq_lens_tensor().tolist() == [21, 21]
+    assert c.block_tables_tensor().data_ptr() == base
+    rows = c.block_tables_tensor()
+    assert rows[0, :2].tolist() == c.tables[1].blocks and rows[1, :2].tolist() == c.tables[0].blocks
+    assert c._write_slots.tolist() == [[c.tables[1].slot(20)], [c.tables[0].slot(20)]]
+
+
+def test_write_scatters_to_the_advanced_slots():
+    c = _cache()
+    c.advance(5, batch_size=2)
+    rng = np.random.default_rng(0)
+    k = torch.from_numpy(rng.standard_normal((2, 2, 5, 128)).astype(np.float16))
+    v = torch.from_numpy(rng.standard_normal((2, 2, 5, 128)).astype(np.float16))
+    c.write(1, k, v)
+    for b in range(2):
+        for p in range(5):
+            s = c.tables[b].slot(p)
+            assert torch.equal(c._flat_k[1][s], k[b, :, p])
+            assert torch.equal(c._flat_v[1][s], v[b, :, p])
+    assert c._flat_k[0].abs().sum() == 0
+
+
+def test_capacity_is_enforced_and_rewind_keeps_blocks():
+    c = _cache(batch=1, cap=32)
+    c.advance(30, batch_size=1)
+    blocks = list(c.tables[0].blocks)
+    c.rewind(10)
+    assert c.seq_lens_tensor().tolist() == [10] and c.tables[0].blocks == blocks
+    c.advance(22, batch_size=1)
+    assert c.tables[0].blocks == blocks
+    with pytest.raises(RuntimeError):
+        c.advance(1, batch_size=1)          # 33 tokens need a third page: past capacity
