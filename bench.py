@@ -44,6 +44,11 @@ CONFIGS = {
     "flat": dict(batch=512, ctx=512, kind="fp16", workload="fp16 paged decode B512 x 512"),
     "c4": dict(batch=16, ctx=16384, kind="int8",
                workload="INT8 paged decode B16 x 16384 (fp32 scales, fp16 last-page K residual)"),
+    # BASELINE configuration 5, second part: a whole decode step of the
+    # Qwen2.5-1.5B geometry (28 layers, random weights) under one HIP graph.
+    "step": dict(batch=16, ctx=8192, kind="step",
+                 workload="full decode step, Qwen2.5-1.5B geometry (28 layers, hidden 1536, "
+                          "vocab 151936, random init), B16 x 8K, HIP graph bucket 8192"),
     "c5": dict(batch=8, ctx=32768, kind="sparse", ratio=0.5,
                workload="sparse 50% paged decode B8 x 32768 (page index + top-k + page-subset "
                         "attention)"),
@@ -267,6 +272,8 @@ def main():
         calibrate_copy(args.calibrate_copy)
         return
     cfg = CONFIGS[args.config]
+    if cfg["kind"] == "step":
+        return bench_step(cfg, args)
     layers = max(1, args.layers)
     tables, seq, pools, max_len = build_workload(cfg, layers, contiguous=args.tables == "contiguous")
     lens = seq.cpu().numpy()
@@ -332,6 +339,66 @@ def main():
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(cfg, tables, seq, pools[0], args.cpu_seqs)
+    print(json.dumps(result))
+
+
+def bench_step(cfg, args):
+    """Whole decode steps through the graph runner: every step is the cache's
+    host bookkeeping, one graph replay (28 layers: GEMMs, RoPE, the K/V write,
+    the HIP paged decode) and the greedy argmax, for B sequences at ~ctx."""
+    import torch
+
+    from latentserve_amd.runtime.hip_graph import GraphedDecoder
+    from latentserve_amd.runtime.qwen_decoder import DecoderConfig, QwenDecoder
+
+    b, ctx = cfg["batch"], cfg["ctx"]
+    steps = min(args.steps, 150)
+    warm = min(args.warmup, 20)
+    start = ctx - steps - warm - 2                 # every timed step stays in the one bucket
+    model = QwenDecoder(DecoderConfig())
+    cache = model.allocate_cache(b, ctx)
+    cache.advance(start, batch_size=b)             # the context's slots, filled directly:
+    g = torch.Generator(device="cuda").manual_seed(1)
+    for layer in range(model.cfg.num_layers):      # K/V of a `start`-token context
+        cache.k_pool[layer].normal_(generator=g)
+        cache.v_pool[layer].normal_(generator=g)
+    dec = GraphedDecoder(model, buckets=(ctx,), greedy=True)
+    tok = torch.randint(0, model.cfg.vocab_size, (b, 1), device="cuda", generator=g)
+    slots = list(range(b))
+
+    def one(t):
+        pos = torch.full((b, 1), start + t, dtype=torch.long, device="cuda")
+        return dec.step_greedy(tok, pos, slots)
+
+    for t in range(warm + 1):
+        nxt = one(t)
+        tok.copy_(nxt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(warm + 1, warm + 1 + steps):
+        nxt = one(t)
+        tok.copy_(nxt)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    st = dec.stats()
+    result = {
+        "metric": "full decode step tokens/s (B16 x 8K, Qwen2.5-1.5B geometry)",
+        "value": round(b / dt, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: random-init weights, N(0,1) K/V context, greedy tokens",
+        "config": {"workload": cfg["workload"], "batch": b, "context_start": start,
+                   "layers": model.cfg.num_layers, "graphs": st["graphs"],
+                   "graph_steps": st["graph_steps"], "eager_steps": st["eager_steps"],
+                   "host_ms_last_step": round(dec.last_host_ms, 3)},
+    }
     print(json.dumps(result))
 
 

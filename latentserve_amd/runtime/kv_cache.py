@@ -169,6 +169,17 @@ class PagedKVCache:
         self._write_slots_buf = torch.zeros((spec.max_batch_size, 1), dtype=torch.long,
                                             device=self.device)
         self._table_state: list = [None] * spec.max_batch_size
+        # Host staging for the per-step copies: pinned and double-buffered,
+        # so a step's slots and lengths go up asynchronously while the
+        # previous step still runs (a pageable copy would wait for it).
+        self._staging = None
+        if self.device.type == "cuda":
+            mb = spec.max_batch_size
+            self._staging = [
+                (torch.empty(mb, dtype=torch.long).pin_memory(),
+                 torch.empty(mb, dtype=torch.int32).pin_memory(), torch.cuda.Event())
+                for _ in range(2)]
+            self._stage_i = 0
         self._write_slots: Optional[torch.Tensor] = None
         self._block_tables: Optional[torch.Tensor] = None
         self._seq_lens_tensor: Optional[torch.Tensor] = None
@@ -227,12 +238,27 @@ class PagedKVCache:
         slots_now = [[self.tables[i].slot(p) for p in range(s, s + n)]
                      for i, s in zip(active, starts)]
         b = len(active)
+        if n == 1 and self._staging is not None:
+            pin_slots, pin_lens, ev = self._next_staging()
+            pin_slots[:b] = torch.tensor([s[0] for s in slots_now], dtype=torch.long)
+            self._write_slots_buf[:b, 0].copy_(pin_slots[:b], non_blocking=True)
+            self._write_slots = self._write_slots_buf[:b]
+            self._rebuild_kernel_inputs(pin_lens, ev)
+            return
         if n == 1:
             self._write_slots_buf[:b].copy_(torch.tensor(slots_now, dtype=torch.long))
             self._write_slots = self._write_slots_buf[:b]
         else:
             self._write_slots = torch.tensor(slots_now, dtype=torch.long, device=self.device)
         self._rebuild_kernel_inputs()
+
+    def _next_staging(self):
+        """The pinned buffers not used by the previous step, once the copies
+        that last read them have run."""
+        self._stage_i ^= 1
+        pin_slots, pin_lens, ev = self._staging[self._stage_i]
+        ev.synchronize()
+        return pin_slots, pin_lens, ev
 
     def rewind(self, length: int, slots: Optional[Sequence[int]] = None) -> None:
         """Shorten the active sequences to `length` tokens, keeping their
@@ -244,7 +270,8 @@ class PagedKVCache:
             t.length = length
         self._rebuild_kernel_inputs()
 
-    def _rebuild_kernel_inputs(self) -> None:
+    def _rebuild_kernel_inputs(self, pin_lens: Optional[torch.Tensor] = None,
+                               ev: Optional[torch.cuda.Event] = None) -> None:
         active = self._active
         b = len(active)
         for row, i in enumerate(active):
@@ -258,8 +285,13 @@ class PagedKVCache:
                     self._block_tables_buf[row, :len(blocks)].copy_(
                         torch.tensor(blocks, dtype=torch.int32))
                 self._table_state[row] = state
-        self._seq_lens_buf[:b].copy_(torch.tensor([self.tables[i].length for i in active],
-                                                  dtype=torch.int32))
+        lens = torch.tensor([self.tables[i].length for i in active], dtype=torch.int32)
+        if pin_lens is not None:
+            pin_lens[:b] = lens
+            self._seq_lens_buf[:b].copy_(pin_lens[:b], non_blocking=True)
+            ev.record()
+        else:
+            self._seq_lens_buf[:b].copy_(lens)
         self._block_tables = self._block_tables_buf[:b]
         self._seq_lens_tensor = self._seq_lens_buf[:b]
 
