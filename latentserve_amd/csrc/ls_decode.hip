@@ -402,18 +402,27 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // length arrives.  Any partition of the pages gives the same result
     // (split-K is exact), so the host's only affects speed.
     const bool host_split = !SPARSE && a.pages_per_split > 0;
+    // The loads are unconditional (clamped to a valid entry, the value
+    // discarded when out of range): predicated loads split the control flow,
+    // and the compiler then waits for every outstanding load where the
+    // paths join, which would serialise the first page loads behind each
+    // other.
     int spec_blk = -1;
     const int spec_lo = host_split ? split * a.pages_per_split : 0;
-    if (host_split && (int)threadIdx.x < a.pages_per_split && spec_lo + (int)threadIdx.x < a.max_pages)
-        spec_blk = a.block_tables[(int64_t)b * a.sbt_b + spec_lo + threadIdx.x];
-    // ... and lane u < NB of each wave fetches the block of the wave's own
-    // fixed item u, so its first page loads need neither the table nor the
-    // barrier.
     int first_blk = -1;
-    if (host_split && lane < NB) {
-        const int e = (wv + lane * NWT) / HG;
-        if (e < a.pages_per_split && spec_lo + e < a.max_pages)
-            first_blk = a.block_tables[(int64_t)b * a.sbt_b + spec_lo + e];
+    if (host_split && a.max_pages > 0) {
+        const int32_t* row = a.block_tables + (int64_t)b * a.sbt_b;
+        const int last = a.max_pages - 1;
+        const int te = spec_lo + (int)threadIdx.x;
+        const int tv = row[te < last ? te : last];
+        spec_blk = (int)threadIdx.x < a.pages_per_split && te <= last ? tv : -1;
+        // ... and lane u < NB of each wave fetches the block of the wave's
+        // own fixed item u, so its first page loads need neither the table
+        // nor the barrier.
+        const int e = (wv + (lane < NB ? lane : 0) * NWT) / HG;
+        const int fe = spec_lo + e;
+        const int fv = row[fe < last ? fe : last];
+        first_blk = lane < NB && e < a.pages_per_split && fe <= last ? fv : -1;
     }
 
     const int len = a.seq_lens[b];
@@ -495,18 +504,18 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         }
     };
 
-    // Query operands of the group's heads: row c (zero beyond n_rep),
-    // channels 32j+8g..+8.
+    // Query operands of the group's heads: row c, channels 32j+8g..+8.
+    // Rows past n_rep repeat row 0: their (finite) scores fill MFMA columns
+    // whose results are never stored, and not masking them keeps the loads
+    // free of any use before the first pages are requested.
     h4 qh[HG][8];
 #pragma unroll
     for (int hh = 0; hh < HG; ++hh) {
-        const bool row_ok = c < a.NR;
-        const half_t* qp =
-            a.q + (int64_t)b * a.sq_b + (int64_t)(h0 + hh) * a.sq_h + (int64_t)c * a.sq_r + 8 * g;
+        const half_t* qp = a.q + (int64_t)b * a.sq_b + (int64_t)(h0 + hh) * a.sq_h +
+                           (int64_t)(c < a.NR ? c : 0) * a.sq_r + 8 * g;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            u4 t = {0u, 0u, 0u, 0u};
-            if (row_ok) t = *(const u4*)(qp + 32 * j);
+            const u4 t = *(const u4*)(qp + 32 * j);
             qh[hh][2 * j] = as_h4(t.x, t.y);
             qh[hh][2 * j + 1] = as_h4(t.z, t.w);
         }
@@ -543,17 +552,13 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         }
     };
     // The wave's fixed item u (dense walk with the host's split): its block
-    // is in lane u of first_blk.
+    // is in lane u of first_blk.  Returned unchecked: the sequence length is
+    // not needed to request the page (issue_with checks the item afterwards).
     auto resolve_first = [&](int u, int i, int& blk, int& pg, int& hh) {
         hh = HG == 1 ? 0 : i % HG;
         const int e = HG == 1 ? i : i / HG;
-        pg = lo + e;
+        pg = spec_lo + e;
         blk = __builtin_amdgcn_readlane(first_blk, u);
-        if (i >= n_items || !(pg >= 0 && pg < num_pages) || blk < 0 || blk >= a.num_blocks ||
-            (HAS_RES && pg == num_pages - 1 && !res_ok)) {
-            blk = -1;
-            pg = -1;
-        }
     };
     auto resolve_mem = [&](int i, int& blk, int& pg, int& hh) {
         hh = HG == 1 ? 0 : i % HG;
@@ -568,31 +573,46 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
 
     // Three page buffers in rotation: items k+1 and k+2 are in flight while
     // item k is computed, and the item after is being claimed.
-    auto walk = [&](auto resolve) {
+    auto walk = [&](auto resolve, auto first) {
         PageBuf buf[NB];
-        int item[NB], pgs[NB], ok[NB], hds[NB];
+        int item[NB], pgs[NB], blks[NB], hds[NB];
+        // An item is requested from any block id that is safe to read, and
+        // checked against the sequence afterwards, so an fp16 request never
+        // waits for the length (INT8 needs the page to pick its K source).
+        // The item is checked against the sequence when it is computed
+        // (live), not when requested: an fp16 request reads a safe block id
+        // and never waits for the length (INT8 needs the page to pick its K
+        // source, so it checks first).
+        auto live = [&](int slot) {
+            const int it = item[slot], blk = blks[slot], pg = pgs[slot];
+            return it < n_items && blk >= 0 && blk < a.num_blocks && pg >= 0 && pg < num_pages &&
+                   !(HAS_RES && pg == num_pages - 1 && !res_ok);
+        };
         auto issue_with = [&](auto res, int slot, int it) {
             int blk, pg, hh;
             item[slot] = it;
             res(it, blk, pg, hh);
-            ok[slot] = blk >= 0;
-            pgs[slot] = pg;
             hds[slot] = hh;
-            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], ok[slot] ? blk : 0, ok[slot] ? pg : -1,
-                                           num_pages, b, h0 + hh, g, c);
+            blks[slot] = blk;
+            pgs[slot] = pg;
+            if (KIND == KV_FP16) {
+                const int safe_blk = (unsigned)blk < (unsigned)a.num_blocks ? blk : 0;
+                load_page<KIND, ASYM, HAS_RES>(a, buf[slot], safe_blk, -1, num_pages, b, h0 + hh,
+                                               g, c);
+            } else {
+                const bool ok = live(slot);
+                load_page<KIND, ASYM, HAS_RES>(a, buf[slot], ok ? blk : 0, ok ? pg : -1,
+                                               num_pages, b, h0 + hh, g, c);
+            }
         };
         auto issue = [&](int slot, int it) { issue_with(resolve, slot, it); };
         // The first items are fixed (wave wv takes wv, wv + NWT, ...): their
         // blocks come straight from the table, so their loads are in flight
         // while the group fills the item table and meets at the barrier.
 #pragma unroll
-        for (int u = 0; u < PF_DEPTH; ++u) {
-            if (spec_ok)
-                issue_with([&](int i, int& blk, int& pg, int& hh) { resolve_first(u, i, blk, pg, hh); },
-                           u, wv + u * NWT);
-            else
-                issue_with(resolve_mem, u, wv + u * NWT);
-        }
+        for (int u = 0; u < PF_DEPTH; ++u)
+            issue_with([&](int i, int& blk, int& pg, int& hh) { first(u, i, blk, pg, hh); }, u,
+                       wv + u * NWT);
         fill_table();
         __syncthreads();
         int it_n = wv + PF_DEPTH * NWT;
@@ -608,14 +628,15 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 // computed even when dead (every token masked, a no-op on the
                 // state): a skipped buffer would leave its loads unwaited and
                 // force conservative waits on the next reuse of its registers
-                const int live_len = ok[u] ? len : 0;
+                const bool ok_u = live(u);
+                const int live_len = ok_u ? len : 0;
 #pragma unroll
                 for (int hh = 0; hh < HG; ++hh) {
                     if (hds[u] == hh) {
                         if (ABL == 1 || ABL == 2)
                             consume_page(buf[u], st[hh]);
                         else
-                            compute_page<KIND, ASYM>(buf[u], st[hh], qh[hh], pgs[u],
+                            compute_page<KIND, ASYM>(buf[u], st[hh], qh[hh], ok_u ? pgs[u] : -1,
                                                      live_len, scale_log2, g, sm.kscale[wv]);
                     }
                 }
@@ -624,10 +645,17 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             }
         }
     };
-    if (cached)
-        walk(resolve_lds);
+    // Separate instantiations for the fast path (the host's split covers the
+    // sequence and the item table fits in LDS) and the general ones, so no
+    // fallback load shares the fast path's control flow.
+    auto first_fixed = [&](int u, int i, int& blk, int& pg, int& hh) { resolve_first(u, i, blk, pg, hh); };
+    auto first_mem = [&](int, int i, int& blk, int& pg, int& hh) { resolve_mem(i, blk, pg, hh); };
+    if (cached && spec_ok)
+        walk(resolve_lds, first_fixed);
+    else if (cached)
+        walk(resolve_lds, first_mem);
     else
-        walk(resolve_mem);
+        walk(resolve_mem, first_mem);
 
     const int NR = a.NR;
     const bool single = S == 1;
