@@ -22,8 +22,11 @@
  *   res_rows    [B] int32 (row of k_residual holding each sequence's last page)
  *   out         [B, H_kv, n_rep, 128] fp16        out_strides[3] = (b, h, r)
  *   workspace   fp32 scratch of ls_decode_workspace_bytes() bytes, 256-byte
- *               aligned (one record per (b, h, split): acc[n_rep][128],
- *               m[16], l[16]); needed only when num_splits > 1
+ *               aligned (B * num_splits * H_kv records of acc[n_rep][128],
+ *               m[16], l[16]: a split workgroup's partials, indexed by its
+ *               slot among its KV head's B * num_splits workgroups, which
+ *               the kernel deals to sequences in proportion to their
+ *               lengths); needed only when num_splits > 1
  *   counters    int32 [B * H_kv] (larger is fine), zero before the first
  *               call; every call leaves it zero again (per (sequence, head):
  *               the count of split workgroups that have stored their

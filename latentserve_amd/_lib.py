@@ -14,7 +14,8 @@ from typing import Optional
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liblatentserve_hip.so")
+# LATENTSERVE_HIP_LIB points at another build of the same ABI (A/B runs).
+LIB_PATH = os.environ.get("LATENTSERVE_HIP_LIB") or os.path.join(HERE, "liblatentserve_hip.so")
 
 _VP = ctypes.c_void_p
 _I64P = ctypes.POINTER(ctypes.c_int64)

@@ -36,7 +36,7 @@ struct DecodeParams {
     int num_sel;
     float ratio;
     int recent;
-    float* work;                       // [B, H, S] records of NR*128 + 32 floats:
+    float* work;                       // [B * S, H] records of NR*128 + 32 floats:
                                        // acc[NR][128], m[16] (natural log), l[16]
     int pages_per_split;               // > 0: dense walk partition given by the host
     int32_t* counters;                 // [B * H], zero at rest, reset by the kernel
@@ -44,7 +44,6 @@ struct DecodeParams {
     int64_t so_b, so_h, so_r;
     int B, H, NR, num_splits;
     float scale;
-    int fuse;                          // merge splits in the last-arriving group
 };
 
 struct CombineParams {

@@ -362,6 +362,108 @@ __device__ __forceinline__ void consume_page(const PageBuf& buf, WaveState& st) 
     st.m = 0.f;
 }
 
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ long long wave_sum_l(long long v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ int wave_excl_scan_i(int v, int lane) {
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    return x - v;
+}
+
+struct GroupWork {
+    int len;      // its length
+    int b;        // sequence served
+    int s;        // split index within the sequence
+    int n;        // groups serving the sequence
+    int first;    // index of its first group among the head group's B * S
+};
+
+// Deal the B * S groups of a head group over the sequences: one each, the
+// rest in proportion to their pages (floor), the few left over to the first
+// sequences.  Every wave of every group computes the same deal from
+// seq_lens (lanes take contiguous runs of sequences), so no group needs to
+// hear from another.  Equal lengths give S groups each: the host's grid.
+// lane_len: seq_lens[lane] (lane < B), loaded by the caller ahead of its
+// page requests (loads return in order, so a length requested after them
+// would wait for the pages).
+__device__ GroupWork deal_groups(const DecodeParams& a, int w_id, int lane, int lane_len) {
+    const int B = a.B, S = a.num_splits;
+    const int W = B * S;
+    auto pages_of_len = [&](int len) {
+        int p = len > 0 ? (len + PAGE - 1) / PAGE : 0;
+        return p < a.max_pages ? p : a.max_pages;
+    };
+    GroupWork r = {0, 0, 0, 1, 0};
+    if (B <= WAVE) {
+        // one sequence a lane: each length is read once
+        const int my_len = lane < B ? lane_len : 0;
+        const int p = lane < B ? pages_of_len(my_len) : 0;
+        const long long T = wave_sum_l(p);
+        int n = 0;
+        if (lane < B) n = T > 0 ? 1 + (int)((long long)(W - B) * p / T) : S;
+        const int left = W - wave_sum_i(n);            // 0 <= left < B when T > 0
+        n += lane < left ? 1 : 0;
+        const int pos = wave_excl_scan_i(n, lane);
+        const bool mine = lane < B && w_id >= pos && w_id < pos + n;
+        const unsigned long long who = __ballot(mine);
+        const int src = who ? __builtin_ctzll(who) : 0;
+        r.b = src;
+        r.len = __shfl(my_len, src);
+        r.n = __shfl(n, src);
+        r.first = __shfl(pos, src);
+        r.s = w_id - r.first;
+        return r;
+    }
+    // longer batches: lanes take contiguous runs of sequences
+    const int per_lane = (B + WAVE - 1) / WAVE;
+    const int b0 = lane * per_lane < B ? lane * per_lane : B;
+    const int b1 = b0 + per_lane < B ? b0 + per_lane : B;
+    long long part = 0;
+    for (int i = b0; i < b1; ++i) part += pages_of_len(a.seq_lens[i]);
+    const long long T = wave_sum_l(part);
+    auto base_n = [&](int p) { return T > 0 ? 1 + (int)((long long)(W - B) * p / T) : S; };
+    int mine_n = 0;
+    for (int i = b0; i < b1; ++i) mine_n += base_n(pages_of_len(a.seq_lens[i]));
+    const int left = W - wave_sum_i(mine_n);
+    const int run = mine_n + ((b1 < left ? b1 : left) - (b0 < left ? b0 : left));
+    int pos = wave_excl_scan_i(run, lane);
+    bool found = false;
+    if (w_id >= pos && w_id < pos + run) {
+        for (int i = b0; i < b1; ++i) {
+            const int n = base_n(pages_of_len(a.seq_lens[i])) + (i < left ? 1 : 0);
+            if (w_id < pos + n) {
+                r.b = i;
+                r.s = w_id - pos;
+                r.n = n;
+                r.first = pos;
+                found = true;
+                break;
+            }
+            pos += n;
+        }
+    }
+    const unsigned long long who = __ballot(found);
+    const int src = who ? __builtin_ctzll(who) : 0;
+    r.b = __shfl(r.b, src);
+    r.s = __shfl(r.s, src);
+    r.n = __shfl(r.n, src);
+    r.first = __shfl(r.first, src);
+    r.len = a.seq_lens[r.b];
+    return r;
+}
+
 // Claim the next item of the group for the calling wave: an LDS atomic by
 // lane 0.  The result stays in lane 0's register until claimed_item()
 // reads it one iteration later, off the critical path.
@@ -392,7 +494,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     const int lane = threadIdx.x % WAVE;
     const int h0 = (blockIdx.x % n_hg) * HG;
     const int split = blockIdx.x / n_hg;
-    const int b = blockIdx.y;
+    const int hb = blockIdx.y;          // the host grid's sequence (speculation)
     const int g = lane >> 4, c = lane & 15;
     const int S = a.num_splits;
     if (threadIdx.x == 0) sm.claim = NB * NWT;      // items below were assigned statically
@@ -411,7 +513,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     const int spec_lo = host_split ? split * a.pages_per_split : 0;
     int first_blk = -1;
     if (host_split && a.max_pages > 0) {
-        const int32_t* row = a.block_tables + (int64_t)b * a.sbt_b;
+        const int32_t* row = a.block_tables + (int64_t)hb * a.sbt_b;
         const int last = a.max_pages - 1;
         const int te = spec_lo + (int)threadIdx.x;
         const int tv = row[te < last ? te : last];
@@ -425,7 +527,69 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         first_blk = lane < NB && e < a.pages_per_split && fe <= last ? fv : -1;
     }
 
-    const int len = a.seq_lens[b];
+    // The lengths the deal reads (one a lane for batches up to 64).
+    int lane_len = 0;
+    if (!SPARSE && a.B <= WAVE) lane_len = a.seq_lens[lane < a.B ? lane : 0];
+
+    // Query operands of the group's heads: row c, channels 32j+8g..+8.
+    // Rows past n_rep repeat row 0: their (finite) scores fill MFMA columns
+    // whose results are never stored, and not masking them keeps the loads
+    // free of any use before the first pages are requested.
+    // (The host grid's sequence, which the deal keeps for equal lengths, so
+    // the loads need not wait for the deal; reloaded below if it moved.)
+    h4 qh[HG][8];
+    auto load_q = [&](int bq) {
+#pragma unroll
+    for (int hh = 0; hh < HG; ++hh) {
+        const half_t* qp = a.q + (int64_t)bq * a.sq_b + (int64_t)(h0 + hh) * a.sq_h +
+                           (int64_t)(c < a.NR ? c : 0) * a.sq_r + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u4 t = *(const u4*)(qp + 32 * j);
+            qh[hh][2 * j] = as_h4(t.x, t.y);
+            qh[hh][2 * j + 1] = as_h4(t.z, t.w);
+        }
+    }
+    };
+    load_q(hb);
+
+    // Page buffers in rotation: items k+1 and k+2 are in flight while item k
+    // is computed, and the item after is being claimed.
+    PageBuf buf[NB];
+    int item[NB], pgs[NB], blks[NB], hds[NB];
+    // An fp16 request needs only a block id that is safe to read: the item is
+    // checked against the sequence when it is computed.  (INT8 needs the
+    // page to pick its K source, so it checks first.)
+    auto issue_raw = [&](int slot, int it, int blk, int pg, int hh, bool ok, int bseq,
+                         int npages) {
+        item[slot] = it;
+        blks[slot] = blk;
+        pgs[slot] = pg;
+        hds[slot] = hh;
+        if (KIND == KV_FP16) {
+            const int safe_blk = (unsigned)blk < (unsigned)a.num_blocks ? blk : 0;
+            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], safe_blk, -1, 0, bseq, h0 + hh, g, c);
+        } else {
+            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], ok ? blk : 0, ok ? pg : -1, npages, bseq,
+                                           h0 + hh, g, c);
+        }
+    };
+    // Which sequence and split this group serves: the host grid's for a
+    // page-subset walk, else the length-proportional deal.
+    GroupWork gw;
+    if (SPARSE) {
+        gw.b = hb;
+        gw.s = split;
+        gw.n = S;
+        gw.first = hb * S;
+        gw.len = a.seq_lens[hb];
+    } else {
+        gw = deal_groups(a, hb * S + split, lane, lane_len);
+    }
+    const int b = gw.b;
+    const int Sb = gw.n;
+    const int len = gw.len;
+    if (b != hb) load_q(b);
     int num_pages = (len + PAGE - 1) / PAGE;
     num_pages = num_pages < a.max_pages ? num_pages : a.max_pages;
     bool res_ok = false;
@@ -451,12 +615,25 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             n_list = want < a.num_sel ? want : a.num_sel;
         }
     }
-    // Pages per split: the host's when it covers this sequence, else derived
-    // here from the length (kernels/gqa/paged_decode.py:564-568).
-    const bool spec_ok = host_split && num_pages <= S * a.pages_per_split;
-    const int per = spec_ok ? a.pages_per_split : (n_list + S - 1) / S;
-    const int lo = spec_ok ? spec_lo : split * per;
-    const int hi = lo + per < n_list ? lo + per : n_list;
+    // Pages of this split: the host's partition when the deal kept the host
+    // grid for this group and the host's split covers the sequence (its
+    // speculative table loads are then the group's own); else S_b even
+    // shares of the length (kernels/gqa/paged_decode.py:564-568 derives the
+    // split on the device the same way).
+    const bool spec_ok = host_split && b == hb && Sb == S && gw.s == split &&
+                         num_pages <= S * a.pages_per_split;
+    int lo, hi;
+    if (spec_ok) {
+        lo = spec_lo;
+        hi = lo + a.pages_per_split < n_list ? lo + a.pages_per_split : n_list;
+    } else if (SPARSE || Sb == S) {
+        const int per = (n_list + S - 1) / S;
+        lo = gw.s * per;
+        hi = lo + per < n_list ? lo + per : n_list;
+    } else {
+        lo = (int)((long long)gw.s * n_list / Sb);
+        hi = (int)((long long)(gw.s + 1) * n_list / Sb);
+    }
     const int n_ent = hi > lo ? hi - lo : 0;
     const int n_items = n_ent * HG;
 
@@ -504,22 +681,6 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         }
     };
 
-    // Query operands of the group's heads: row c, channels 32j+8g..+8.
-    // Rows past n_rep repeat row 0: their (finite) scores fill MFMA columns
-    // whose results are never stored, and not masking them keeps the loads
-    // free of any use before the first pages are requested.
-    h4 qh[HG][8];
-#pragma unroll
-    for (int hh = 0; hh < HG; ++hh) {
-        const half_t* qp = a.q + (int64_t)b * a.sq_b + (int64_t)(h0 + hh) * a.sq_h +
-                           (int64_t)(c < a.NR ? c : 0) * a.sq_r + 8 * g;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const u4 t = *(const u4*)(qp + 32 * j);
-            qh[hh][2 * j] = as_h4(t.x, t.y);
-            qh[hh][2 * j + 1] = as_h4(t.z, t.w);
-        }
-    }
     const float scale_log2 = a.scale * LOG2E;
 
     WaveState st[HG];
@@ -571,44 +732,25 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         }
     };
 
-    // Three page buffers in rotation: items k+1 and k+2 are in flight while
-    // item k is computed, and the item after is being claimed.
+    auto live = [&](int slot) {
+        const int it = item[slot], blk = blks[slot], pg = pgs[slot];
+        return it < n_items && blk >= 0 && blk < a.num_blocks && pg >= 0 && pg < num_pages &&
+               !(HAS_RES && pg == num_pages - 1 && !res_ok);
+    };
     auto walk = [&](auto resolve, auto first) {
-        PageBuf buf[NB];
-        int item[NB], pgs[NB], blks[NB], hds[NB];
-        // An item is requested from any block id that is safe to read, and
-        // checked against the sequence afterwards, so an fp16 request never
-        // waits for the length (INT8 needs the page to pick its K source).
-        // The item is checked against the sequence when it is computed
-        // (live), not when requested: an fp16 request reads a safe block id
-        // and never waits for the length (INT8 needs the page to pick its K
-        // source, so it checks first).
-        auto live = [&](int slot) {
-            const int it = item[slot], blk = blks[slot], pg = pgs[slot];
-            return it < n_items && blk >= 0 && blk < a.num_blocks && pg >= 0 && pg < num_pages &&
-                   !(HAS_RES && pg == num_pages - 1 && !res_ok);
-        };
         auto issue_with = [&](auto res, int slot, int it) {
             int blk, pg, hh;
-            item[slot] = it;
             res(it, blk, pg, hh);
-            hds[slot] = hh;
-            blks[slot] = blk;
-            pgs[slot] = pg;
-            if (KIND == KV_FP16) {
-                const int safe_blk = (unsigned)blk < (unsigned)a.num_blocks ? blk : 0;
-                load_page<KIND, ASYM, HAS_RES>(a, buf[slot], safe_blk, -1, num_pages, b, h0 + hh,
-                                               g, c);
-            } else {
-                const bool ok = live(slot);
-                load_page<KIND, ASYM, HAS_RES>(a, buf[slot], ok ? blk : 0, ok ? pg : -1,
-                                               num_pages, b, h0 + hh, g, c);
-            }
+            const bool ok = KIND == KV_FP16 ? true
+                                             : (it < n_items && blk >= 0 && blk < a.num_blocks &&
+                                                pg >= 0 && pg < num_pages &&
+                                                !(HAS_RES && pg == num_pages - 1 && !res_ok));
+            issue_raw(slot, it, blk, pg, hh, ok, b, num_pages);
         };
         auto issue = [&](int slot, int it) { issue_with(resolve, slot, it); };
         // The first items are fixed (wave wv takes wv, wv + NWT, ...): their
-        // blocks come straight from the table, so their loads are in flight
-        // while the group fills the item table and meets at the barrier.
+        // loads are in flight while the group fills the item table and meets
+        // at the barrier.
 #pragma unroll
         for (int u = 0; u < PF_DEPTH; ++u)
             issue_with([&](int i, int& blk, int& pg, int& hh) { first(u, i, blk, pg, hh); }, u,
@@ -658,7 +800,8 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         walk(resolve_mem, first_mem);
 
     const int NR = a.NR;
-    const bool single = S == 1;
+    const bool single = Sb == 1;
+    const int w_rec = gw.first + gw.s;   // this group's record slot among the head group's B * S
     if (ABL >= 2) {                      // diagnostic: no merge, no partials
 #pragma unroll
         for (int hh = 0; hh < HG; ++hh)
@@ -667,7 +810,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         if (!single && threadIdx.x < (unsigned)HG) {
             const int64_t bh = (int64_t)b * H + h0 + threadIdx.x;
             if (__hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT) == S - 1)
+                                       __HIP_MEMORY_SCOPE_AGENT) == Sb - 1)
                 __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
@@ -675,8 +818,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
 
     // ---- merge the waves' states in LDS (all heads at once); each wave
     // stores its state as soon as its walk ends ----
-    // One record per (b, h, split): acc[NR][128], m[16], l[16].  Every cache
-    // line of a record is written by this group alone.
+    // One record per (group, head): acc[NR][128], m[16], l[16], at slot
+    // (w_rec * H + h); the groups of a sequence have adjacent slots.  Every
+    // cache line of a record is written by this group alone.
     const int64_t rec = (int64_t)NR * HEAD_DIM + 2 * MAX_NREP;
     float lrow[HG];
 #pragma unroll
@@ -721,26 +865,19 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             lt += sm.l[hh][u][r] * wt;
             at += sm.acc[hh][u][r][d] * wt;
         }
-        const int64_t bh = (int64_t)b * H + h0 + hh;
-        float* pacc = a.work + (bh * S + split) * rec;
+        float* pacc = a.work + ((int64_t)w_rec * H + h0 + hh) * rec;
         float* pm = pacc + NR * HEAD_DIM;
         float* pl = pm + MAX_NREP;
         if (single) {
             a.out[(int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h + (int64_t)r * a.so_r + d] =
                 (half_t)(at / fmaxf(lt, 1e-20f));
-        } else if (a.fuse) {
+        } else {
             // Device-coherent (write-through) stores: the group that merges
             // may run on another XCD, whose L2 does not see this one's.
             store_coherent(pacc + ri, at);
             if (d == 0) {
                 store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
                 store_coherent(pl + r, lt);
-            }
-        } else {
-            pacc[ri] = at;
-            if (d == 0) {
-                pm[r] = mg * LN2;
-                pl[r] = lt;
             }
         }
     }
@@ -750,17 +887,15 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // The records above bypass the non-coherent L2 path, so ordering needs
     // only their completion before the arrival count: no whole-L2 writeback
     // or invalidate (which a device-scope fence would issue in every group).
-    if (a.fuse) {
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     if (threadIdx.x < (unsigned)HG) {
         const int64_t bh = (int64_t)b * H + h0 + threadIdx.x;
         const int prev = __hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
-        sm.is_last[threadIdx.x] = prev == S - 1;
+        sm.is_last[threadIdx.x] = prev == Sb - 1;
     }
     __syncthreads();
     // 256 threads per head: a group of HG heads merges each head it closed
@@ -768,12 +903,12 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     const int hh = threadIdx.x / 256, t256 = threadIdx.x % 256;
     if (!sm.is_last[hh]) return;
     const int64_t bh = (int64_t)b * H + h0 + hh;
-    if (a.fuse) {
+    {
         // The records were written through to memory and no group has read
         // their lines in this launch, so plain vector loads see them.
-        const float* recs = a.work + bh * S * rec;
-        combine_partials<4>(recs, recs + NR * HEAD_DIM, recs + NR * HEAD_DIM + MAX_NREP, S, NR,
-                            rec, HEAD_DIM, rec,
+        const float* recs = a.work + ((int64_t)gw.first * H + h0 + hh) * rec;
+        combine_partials<4>(recs, recs + NR * HEAD_DIM, recs + NR * HEAD_DIM + MAX_NREP, Sb, NR,
+                            (int64_t)H * rec, HEAD_DIM, (int64_t)H * rec,
                             a.out + (int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h, 0, a.so_r,
                             t256);
     }
@@ -852,43 +987,8 @@ static hipError_t launch_kernel(const DecodeParams& a, hipStream_t stream) {
     return launch_t<KV_INT8, false, false, false>(a, stream);
 }
 
-// LATENTSERVE_HIP_COMBINE=separate merges the splits in a second launch
-// instead of in the decode kernel's last-arriving group (for comparison).
-static bool fused_combine() {
-    static const int fused = [] {
-        const char* e = getenv("LATENTSERVE_HIP_COMBINE");
-        return (e && strcmp(e, "separate") == 0) ? 0 : 1;
-    }();
-    return fused != 0;
-}
-
-hipError_t launch_decode(const DecodeParams& a_in, hipStream_t stream) {
-    DecodeParams a = a_in;
-    a.fuse = fused_combine() ? 1 : 0;
-    hipError_t e = launch_kernel(a, stream);
-    if (e != hipSuccess || a.fuse || a.num_splits == 1) return e;
-    CombineParams p;
-    const int64_t rec = (int64_t)a.NR * HEAD_DIM + 2 * MAX_NREP;
-    p.acc = a.work;
-    p.sa_r = HEAD_DIM;
-    p.sa_s = rec;
-    p.sa_h = rec * a.num_splits;
-    p.sa_b = p.sa_h * a.H;
-    p.m = a.work + a.NR * HEAD_DIM;
-    p.l = p.m + MAX_NREP;
-    p.sm_s = rec;
-    p.sm_h = p.sa_h;
-    p.sm_b = p.sa_b;
-    p.out = a.out;
-    p.out_f32 = 0;
-    p.so_b = a.so_b;
-    p.so_h = a.so_h;
-    p.so_r = a.so_r;
-    p.B = a.B;
-    p.H = a.H;
-    p.S = a.num_splits;
-    p.NR = a.NR;
-    return launch_combine(p, stream);
+hipError_t launch_decode(const DecodeParams& a, hipStream_t stream) {
+    return launch_kernel(a, stream);
 }
 
 hipError_t launch_combine(const CombineParams& p, hipStream_t stream) {

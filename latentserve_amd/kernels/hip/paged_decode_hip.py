@@ -25,11 +25,14 @@ from latentserve_amd.kernels.gqa import _scratch as scratch
 HEAD_DIM = 128
 PAGE = 16
 MAX_NREP = 16
-# Waves per (sequence, head, split) in the decode kernel (each walks every
-# NW-th page of its split); must match NWAVES in csrc/ls_decode.hip.
-WAVES_PER_GROUP = 4
 MAX_SPLITS = 1024
-WAVES_PER_CU = 8
+# (sequence, KV head, split) units per CU the split count aims at: the fp16
+# kernel runs one workgroup per split of a KV-head pair, so two units a CU is
+# one workgroup per CU, the measured optimum (more groups than CUs leaves a
+# second, partial round).
+UNITS_PER_CU = 2
+# Fewest pages a split is given.
+MIN_SPLIT_PAGES = 8
 
 _CU_COUNT: dict = {}
 
@@ -45,15 +48,13 @@ def choose_splits(batch: int, kv_heads: int, num_pages: int,
                   device: Optional[torch.device] = None) -> int:
     """Splits per (sequence, KV head) for the MI355X kernel.
 
-    One resident round of waves: every (sequence, head, split) is four
-    waves, and the fp16 kernel's register budget keeps WAVES_PER_CU of them
-    on a CU; never so many splits that a wave gets fewer than two pages.
-    Fixed by (batch, heads, pages) alone, so a captured graph can pin it per
-    context bucket.
+    Enough (sequence, head, split) units for UNITS_PER_CU per CU, never a
+    split of fewer than MIN_SPLIT_PAGES pages.  Fixed by (batch, heads,
+    pages) alone, so a captured graph can pin it per context bucket.
     """
     cus = _cus(device) if device is not None and torch.cuda.is_available() else 256
-    by_cus = -(-(WAVES_PER_CU * cus) // max(1, batch * kv_heads * WAVES_PER_GROUP))
-    by_pages = max(1, num_pages // (2 * WAVES_PER_GROUP))
+    by_cus = -(-(UNITS_PER_CU * cus) // max(1, batch * kv_heads))
+    by_pages = max(1, num_pages // MIN_SPLIT_PAGES)
     return max(1, min(MAX_SPLITS, by_cus, by_pages))
 
 
