@@ -13,7 +13,7 @@
  * Layouts (strides in elements, innermost dimension unit-stride):
  *   q           [B, H_kv, n_rep, 128] fp16        strides q_strides[3] = (b, h, r)
  *   k/v pool    [num_blocks, 16, H_kv, 128]       strides kv_strides[3] = (block, token, head)
- *   block_tables[B, max_pages] int32              row stride bt_stride
+ *   block_tables[B, max_pages] int32              row stride bt_stride; max_pages <= 2^24
  *   seq_lens    [B] int32
  *   k_scale     [num_blocks, H_kv, 128] fp32      ks_strides[2] = (block, head)
  *   v_scale     [num_blocks, 16, H_kv]  fp32      vs_strides[3] = (block, token, head)

@@ -70,6 +70,8 @@ int check_common(const void* q, const int64_t* q_strides, const void* k_pool, co
         return fail(LS_ERR_INVALID, "num_splits must be >= 1, got %d", num_splits);
     if (num_blocks < 1) return fail(LS_ERR_INVALID, "num_blocks must be >= 1");
     if (max_pages < 1) return fail(LS_ERR_INVALID, "max_pages (block-table width) must be >= 1");
+    if (max_pages > (1 << 24))
+        return fail(LS_ERR_INVALID, "max_pages (block-table width) must be <= 2^24");
     if (!rows_aligned(q, q_strides, 3, 2, 16))
         return fail(LS_ERR_INVALID, "q rows must be 16-byte aligned");
     if (!rows_aligned(k_pool, kv_strides, 3, kv_elem, kv_elem == 2 ? 16 : 8) ||

@@ -382,6 +382,25 @@ __device__ __forceinline__ int wave_excl_scan_i(int v, int lane) {
     return x - v;
 }
 
+// Inclusive prefix sum over the wave's lanes in lane order, and the wave's
+// total: a scan within each row of 16 lanes by DPP row shifts (a lane whose
+// source is outside its row adds 0), then the rows' totals by readlane.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int wave_incl_scan_dpp(int x, int lane, int& total) {
+    x += dpp_i<0x111>(x);    // row_shr:1
+    x += dpp_i<0x112>(x);    // row_shr:2
+    x += dpp_i<0x114>(x);    // row_shr:4
+    x += dpp_i<0x118>(x);    // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31),
+              r2 = __builtin_amdgcn_readlane(x, 47), r3 = __builtin_amdgcn_readlane(x, 63);
+    total = r0 + r1 + r2 + r3;
+    const int row = lane >> 4;
+    return x + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+}
+
 struct GroupWork {
     int len;      // its length
     int b;        // sequence served
@@ -407,22 +426,30 @@ __device__ GroupWork deal_groups(const DecodeParams& a, int w_id, int lane, int 
     };
     GroupWork r = {0, 0, 0, 1, 0};
     if (B <= WAVE) {
-        // one sequence a lane: each length is read once
+        // one sequence a lane: each length is read once.  Pages per lane
+        // are at most max_pages < 2^24, so every sum fits 32 bits, and the
+        // quotient (W - B) * p / T (numerator < 2^40) is taken in double:
+        // correctly rounded, it cannot reach the next integer, since a
+        // non-integral quotient is at least 1/T below it.
         const int my_len = lane < B ? lane_len : 0;
         const int p = lane < B ? pages_of_len(my_len) : 0;
-        const long long T = wave_sum_l(p);
+        int T;
+        (void)wave_incl_scan_dpp(p, lane, T);
         int n = 0;
-        if (lane < B) n = T > 0 ? 1 + (int)((long long)(W - B) * p / T) : S;
-        const int left = W - wave_sum_i(n);            // 0 <= left < B when T > 0
+        if (lane < B)
+            n = T > 0 ? 1 + (int)((double)(W - B) * (double)p / (double)T) : S;
+        int sum_n;
+        const int incl = wave_incl_scan_dpp(n, lane, sum_n);
+        const int left = W - sum_n;                    // 0 <= left < B when T > 0
+        const int pos = incl - n + (lane < left ? lane : left);
         n += lane < left ? 1 : 0;
-        const int pos = wave_excl_scan_i(n, lane);
         const bool mine = lane < B && w_id >= pos && w_id < pos + n;
         const unsigned long long who = __ballot(mine);
         const int src = who ? __builtin_ctzll(who) : 0;
         r.b = src;
-        r.len = __shfl(my_len, src);
-        r.n = __shfl(n, src);
-        r.first = __shfl(pos, src);
+        r.len = __builtin_amdgcn_readlane(my_len, src);
+        r.n = __builtin_amdgcn_readlane(n, src);
+        r.first = __builtin_amdgcn_readlane(pos, src);
         r.s = w_id - r.first;
         return r;
     }
@@ -442,8 +469,10 @@ __device__ GroupWork deal_groups(const DecodeParams& a, int w_id, int lane, int 
     bool found = false;
     if (w_id >= pos && w_id < pos + run) {
         for (int i = b0; i < b1; ++i) {
-            const int n = base_n(pages_of_len(a.seq_lens[i])) + (i < left ? 1 : 0);
+            const int li = a.seq_lens[i];
+            const int n = base_n(pages_of_len(li)) + (i < left ? 1 : 0);
             if (w_id < pos + n) {
+                r.len = li;
                 r.b = i;
                 r.s = w_id - pos;
                 r.n = n;
@@ -460,7 +489,10 @@ __device__ GroupWork deal_groups(const DecodeParams& a, int w_id, int lane, int 
     r.s = __shfl(r.s, src);
     r.n = __shfl(r.n, src);
     r.first = __shfl(r.first, src);
-    r.len = a.seq_lens[r.b];
+    // (the length comes from the lane that found it, not a new load: a load
+    // pending here would make the small-batch path, which this one joins,
+    // wait for every outstanding load before its first page request)
+    r.len = __shfl(r.len, src);
     return r;
 }
 

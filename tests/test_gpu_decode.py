@@ -54,6 +54,21 @@ def test_ragged_lengths_match_the_oracle(splits):
     assert_close(run_fp16(case, splits), want, ATOL, RTOL, f"splits={splits}")
 
 
+@pytest.mark.parametrize("batch", [63, 64, 65, 150])
+@pytest.mark.parametrize("splits", [None, 3])
+def test_large_ragged_batches_match_the_oracle(batch, splits):
+    """Split workgroups are dealt to sequences in proportion to their pages,
+    one sequence a lane up to 64 sequences and runs of sequences a lane past
+    that; empty sequences and a few long ones test both deals."""
+    rng = np.random.default_rng(batch)
+    lens = rng.integers(0, 120, batch)
+    lens[::7] = 0
+    lens[3] = 900
+    case = paged_case([int(x) for x in lens], seed=batch)
+    want = oracle.paged_decode(*case, num_splits=1)
+    assert_close(run_fp16(case, splits), want, ATOL, RTOL, f"B={batch} splits={splits}")
+
+
 def test_config1_b1_2048_pool256():
     """B1 x 2048, pool of 256 blocks, permuted table."""
     rng = np.random.default_rng(1)
