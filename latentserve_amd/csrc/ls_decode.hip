@@ -300,25 +300,31 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
         for (int s0 = 0; s0 < S; s0 += CMB_CHUNK) {
             const int n = S - s0 < CMB_CHUNK ? S - s0 : CMB_CHUNK;
             float mv[CMB_CHUNK], lv[CMB_CHUNK], av[CMB_CHUNK][4];
+            // Every slot loads (slots past the last split reread it) and is
+            // masked afterwards: loads under a branch would each wait for
+            // the one before.
 #pragma unroll
             for (int i = 0; i < CMB_CHUNK; ++i) {
-                mv[i] = neg_inf();
-                lv[i] = 0.f;
+                const int64_t sp = s0 + i < S ? s0 + i : S - 1;
+                mv[i] = m[sp * sm_s + r];
+                lv[i] = l[sp * sm_s + r];
+                const float* src = acc + sp * sa_s + r * sa_r + d0;
+                if (VEC == 4) {
+                    const f4 t = *(const f4*)src;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) av[i][e] = 0.f;
-                if (i < n) {
-                    const int64_t sp = (int64_t)(s0 + i);
-                    mv[i] = m[sp * sm_s + r];
-                    lv[i] = l[sp * sm_s + r];
-                    const float* src = acc + sp * sa_s + r * sa_r + d0;
-                    if (VEC == 4) {
-                        const f4 t = *(const f4*)src;
+                    for (int e = 0; e < 4; ++e) av[i][e] = t[e];
+                } else {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) av[i][e] = t[e];
-                    } else {
+                    for (int e = 0; e < 4; ++e) av[i][e] = src[e];
+                }
+            }
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) av[i][e] = src[e];
-                    }
+            for (int i = 0; i < CMB_CHUNK; ++i) {
+                if (i >= n) {
+                    mv[i] = neg_inf();
+                    lv[i] = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) av[i][e] = 0.f;
                 }
             }
             float cm = mg;
