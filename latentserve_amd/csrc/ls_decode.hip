@@ -890,32 +890,52 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     }
     __syncthreads();
 
-    for (int idx = threadIdx.x; idx < HG * NR * HEAD_DIM; idx += WAVE * NWT) {
-        const int hh = idx / (NR * HEAD_DIM), ri = idx % (NR * HEAD_DIM);
-        const int r = ri / HEAD_DIM, d = ri % HEAD_DIM;
-        float mg = neg_inf();
-#pragma unroll
-        for (int u = 0; u < NWT; ++u) mg = fmaxf(mg, sm.m[hh][u][r]);
-        float lt = 0.f, at = 0.f;
-#pragma unroll
-        for (int u = 0; u < NWT; ++u) {
-            const float wt = mg == neg_inf() ? 0.f : fast_exp2(sm.m[hh][u][r] - mg);
-            lt += sm.l[hh][u][r] * wt;
-            at += sm.acc[hh][u][r][d] * wt;
-        }
+    // 256 threads a head; a thread merges four channels of one row, with
+    // all of its loads issued together (rows 8 apart share a thread).
+    static_assert(WAVE * NWT == 256 * HG, "the merge is written for 256 threads a head");
+    {
+        const int hh = threadIdx.x / 256, t256 = threadIdx.x % 256;
+        const int d0 = (t256 % 32) * 4;
         float* pacc = a.work + ((int64_t)w_rec * H + h0 + hh) * rec;
         float* pm = pacc + NR * HEAD_DIM;
         float* pl = pm + MAX_NREP;
-        if (single) {
-            a.out[(int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h + (int64_t)r * a.so_r + d] =
-                (half_t)(at / fmaxf(lt, 1e-20f));
-        } else {
-            // Device-coherent (write-through) stores: the group that merges
-            // may run on another XCD, whose L2 does not see this one's.
-            store_coherent(pacc + ri, at);
-            if (d == 0) {
-                store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
-                store_coherent(pl + r, lt);
+        for (int r = t256 / 32; r < NR; r += 8) {
+            float mv[NWT], lv[NWT];
+            f4 av[NWT];
+#pragma unroll
+            for (int u = 0; u < NWT; ++u) {
+                mv[u] = sm.m[hh][u][r];
+                lv[u] = sm.l[hh][u][r];
+                av[u] = *(const f4*)&sm.acc[hh][u][r][d0];
+            }
+            float mg = neg_inf();
+#pragma unroll
+            for (int u = 0; u < NWT; ++u) mg = fmaxf(mg, mv[u]);
+            float lt = 0.f;
+            f4 at = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < NWT; ++u) {
+                const float wt = mg == neg_inf() ? 0.f : fast_exp2(mv[u] - mg);
+                lt += lv[u] * wt;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) at[e] += av[u][e] * wt;
+            }
+            if (single) {
+                half_t* o = a.out + (int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h +
+                            (int64_t)r * a.so_r + d0;
+                const float inv = 1.f / fmaxf(lt, 1e-20f);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = (half_t)(at[e] * inv);
+            } else {
+                // Device-coherent (write-through) stores: the group that
+                // merges may run on another XCD, whose L2 does not see this
+                // one's.
+#pragma unroll
+                for (int e = 0; e < 4; ++e) store_coherent(pacc + r * HEAD_DIM + d0 + e, at[e]);
+                if (d0 == 0) {
+                    store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
+                    store_coherent(pl + r, lt);
+                }
             }
         }
     }
@@ -937,7 +957,6 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     }
     __syncthreads();
     // 256 threads per head: a group of HG heads merges each head it closed
-    static_assert(WAVE * NWT == 256 * HG, "the fused combine is written for 256 threads a head");
     const int hh = threadIdx.x / 256, t256 = threadIdx.x % 256;
     if (!sm.is_last[hh]) return;
     const int64_t bh = (int64_t)b * H + h0 + hh;

@@ -69,6 +69,19 @@ def test_large_ragged_batches_match_the_oracle(batch, splits):
     assert_close(run_fp16(case, splits), want, ATOL, RTOL, f"B={batch} splits={splits}")
 
 
+@pytest.mark.parametrize("max_len", [None, 4096])
+def test_counters_are_zero_after_every_call(max_len):
+    """The arrival counts are reset by the group that closes each (sequence,
+    head), so back-to-back calls with different split counts (and graph
+    replays) start from zero."""
+    case = paged_case([4096, 4096, 3000, 17], seed=5)
+    want = oracle.paged_decode(*case, num_splits=1)
+    for splits in (8, 8, 3, 16):
+        assert_close(run_fp16(case, splits, max_len), want, ATOL, RTOL, f"splits={splits}")
+        _, _, cnt = hip_mod()._buffers("hip", 4, 2, splits, 6, torch.device("cuda"))
+        assert int(cnt.abs().sum()) == 0, cnt.cpu().numpy()
+
+
 def test_config1_b1_2048_pool256():
     """B1 x 2048, pool of 256 blocks, permuted table."""
     rng = np.random.default_rng(1)
