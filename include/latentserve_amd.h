@@ -237,6 +237,59 @@ int ls_paged_gather(const void* pool, int elem_bytes, const int64_t* kv_strides,
                     const int32_t* seq_lens, void* out, const int64_t* out_strides, int batch,
                     int kv_heads, int head_dim, int page, int length, void* stream);
 
+/* ---- fused elementwise ops of the decode step ----
+ *
+ * fp16 throughout, each product, sum and cast rounded to fp16 where Hugging
+ * Face's Qwen2 computation rounds (kernels/fused_elementwise.py:75-110).
+ * Row-major 2-D operands take a row stride in elements and unit inner
+ * stride. */
+
+/* y[r] = w * fp16(s * rsqrt(mean(s^2) + eps)) with s = x[r], or, when
+ * residual is given, s = fp16(residual[r] + x[r]), also stored to res_out[r]
+ * (residual and res_out both NULL or both given).  x, residual, y, res_out
+ * [rows, n]; w [n].  Replaces rms_norm (kernels/fused_elementwise.py:194-205)
+ * and fused_add_rms_norm (:207-220). */
+int ls_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t res_stride,
+                const void* weight, void* y, int64_t y_stride, void* res_out,
+                int64_t res_out_stride, int rows, int n, float eps, void* stream);
+
+/* out[r] = fp16(fp16(silu(g)) * u), g = gate_up[r, :inter], u = gate_up[r,
+ * inter:2 inter].  Replaces silu_and_mul (kernels/fused_elementwise.py:222-233). */
+int ls_silu_and_mul(const void* gate_up, int64_t gu_stride, void* out, int64_t out_stride,
+                    int rows, int inter, void* stream);
+
+/* RoPE (rotate-half pairing) on q [rows, hq * head_dim] and k [rows, hk *
+ * head_dim] with fp16 cos / sin rows [rows, head_dim] (a table stride of 0
+ * uses one row for all): out = fp16(fp16(x * cos) + fp16(rotate_half(x) *
+ * sin)).  Replaces rope_qk (kernels/fused_elementwise.py:235-252). */
+int ls_rope_qk(const void* q, int64_t q_stride, const void* k, int64_t k_stride, const void* cos,
+               int64_t cos_stride, const void* sin, int64_t sin_stride, void* q_out,
+               int64_t q_out_stride, void* k_out, int64_t k_out_stride, int rows, int hq, int hk,
+               int head_dim, void* stream);
+
+/* One decode token per sequence, straight from the fused q/k/v projection
+ * output qkv [batch, (hq + 2 hk) * head_dim] (row stride qkv_stride): RoPE
+ * as ls_rope_qk at position positions[b] (int64, clamped into the table of
+ * table_rows rows of fp16 cos / sin, row stride table_stride); the rotated
+ * query heads folded to q_out [batch, hk, hq / hk, head_dim] (q_strides[3] =
+ * (b, kv head, row); query head i goes to kv head i / (hq / hk)); the
+ * rotated key and the value stored at flat slot slots[b] (int64, = block *
+ * page + offset; negative or past the pool: not stored) of k_pool / v_pool
+ * [num_blocks, page, hk, head_dim] (kv_strides[3] = (block, token, head)).
+ * With kmin / kmax [num_blocks, hk, head_dim] fp16 (bounds_strides[2] =
+ * (block, head); both NULL to skip), the stored key also updates its page's
+ * K bounds as ls_page_bounds_update does.  Replaces, in one launch, rope_qk
+ * (model/attention/gqa.py:251-253), the paged store of the new rows
+ * (cache/paged_cache.py write, bounds :457-460) and the fold of q to
+ * [B, H_kv, n_rep, D] (model/attention/gqa.py:290-341). */
+int ls_rope_write_decode(const void* qkv, int64_t qkv_stride, const int64_t* positions,
+                         const void* cos, const void* sin, int64_t table_stride, int table_rows,
+                         const int64_t* slots, void* k_pool, void* v_pool,
+                         const int64_t* kv_strides, int num_blocks, int page, void* q_out,
+                         const int64_t* q_strides, void* kmin, void* kmax,
+                         const int64_t* bounds_strides, int batch, int hq, int hk, int head_dim,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,7 +27,7 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -66,6 +66,15 @@ _SIGNATURES = {
     "ls_paged_gather": [
         _VP, _I32, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P, _I32, _I32, _I32, _I32, _I32,
         _VP],
+    "ls_rms_norm": [
+        _VP, _I64, _VP, _I64, _VP, _VP, _I64, _VP, _I64, _I32, _I32, _F32, _VP],
+    "ls_silu_and_mul": [_VP, _I64, _VP, _I64, _I32, _I32, _VP],
+    "ls_rope_qk": [
+        _VP, _I64, _VP, _I64, _VP, _I64, _VP, _I64, _VP, _I64, _VP, _I64, _I32, _I32, _I32, _I32,
+        _VP],
+    "ls_rope_write_decode": [
+        _VP, _I64, _VP, _VP, _VP, _I64, _I32, _VP, _VP, _VP, _I64P, _I32, _I32, _VP, _I64P, _VP,
+        _VP, _I64P, _I32, _I32, _I32, _I32, _VP],
     "ls_combine_splits": [
         _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
 }

@@ -20,6 +20,7 @@
 #include "ls_sparse.h"
 #include "ls_int8_write.h"
 #include "ls_gather.h"
+#include "ls_elementwise.h"
 
 namespace {
 
@@ -132,7 +133,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 5; }
+int ls_abi_version(void) { return 6; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -586,6 +587,134 @@ int ls_paged_gather(const void* pool, int elem_bytes, const int64_t* kv_strides,
     a.L = length;
     a.H = kv_heads;
     return hip_status(ls::launch_gather(a, (hipStream_t)stream), "ls_paged_gather");
+}
+
+int ls_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t res_stride,
+                const void* weight, void* y, int64_t y_stride, void* res_out,
+                int64_t res_out_stride, int rows, int n, float eps, void* stream) {
+    if (!x || !weight || !y) return fail(LS_ERR_INVALID, "null pointer argument");
+    if ((residual == nullptr) != (res_out == nullptr))
+        return fail(LS_ERR_INVALID, "residual and res_out must be given together");
+    if (rows < 0 || rows > 2147483647 || n < 1)
+        return fail(LS_ERR_INVALID, "rows must be >= 0 and n >= 1 (rows %d, n %d)", rows, n);
+    if (!(eps >= 0.f)) return fail(LS_ERR_INVALID, "eps must be >= 0");
+    ls::NormParams a;
+    a.x = x;
+    a.sx = x_stride;
+    a.res = residual;
+    a.sr = res_stride;
+    a.w = weight;
+    a.y = y;
+    a.sy = y_stride;
+    a.res_out = res_out;
+    a.sro = res_out_stride;
+    a.rows = rows;
+    a.n = n;
+    a.eps = eps;
+    a.vec = n % 8 == 0 && aligned(x, 16) && aligned(weight, 16) && aligned(y, 16) &&
+            x_stride % 8 == 0 && y_stride % 8 == 0 &&
+            (!residual || (aligned(residual, 16) && aligned(res_out, 16) && res_stride % 8 == 0 &&
+                           res_out_stride % 8 == 0));
+    return hip_status(ls::launch_rms_norm(a, (hipStream_t)stream), "ls_rms_norm");
+}
+
+int ls_silu_and_mul(const void* gate_up, int64_t gu_stride, void* out, int64_t out_stride,
+                    int rows, int inter, void* stream) {
+    if (!gate_up || !out) return fail(LS_ERR_INVALID, "null pointer argument");
+    if (rows < 0 || rows > 65535 || inter < 1)
+        return fail(LS_ERR_INVALID, "rows must be in [0, 65535] and inter >= 1 (rows %d, inter %d)",
+                    rows, inter);
+    ls::SiluParams a;
+    a.gu = gate_up;
+    a.sgu = gu_stride;
+    a.out = out;
+    a.so = out_stride;
+    a.rows = rows;
+    a.inter = inter;
+    a.vec = inter % 8 == 0 && aligned(gate_up, 16) && aligned(out, 16) && gu_stride % 8 == 0 &&
+            out_stride % 8 == 0;
+    return hip_status(ls::launch_silu_and_mul(a, (hipStream_t)stream), "ls_silu_and_mul");
+}
+
+int ls_rope_qk(const void* q, int64_t q_stride, const void* k, int64_t k_stride, const void* cos,
+               int64_t cos_stride, const void* sin, int64_t sin_stride, void* q_out,
+               int64_t q_out_stride, void* k_out, int64_t k_out_stride, int rows, int hq, int hk,
+               int head_dim, void* stream) {
+    if (!q || !k || !cos || !sin || !q_out || !k_out)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim < 2 || head_dim > 1024 || head_dim % 2 != 0)
+        return fail(LS_ERR_INVALID, "head_dim must be even and in [2, 1024], got %d", head_dim);
+    if (rows < 0 || hq < 0 || hk < 0 || hq + hk < 1 || hq + hk > 65535)
+        return fail(LS_ERR_INVALID, "bad rows or head counts (rows %d, hq %d, hk %d)", rows, hq,
+                    hk);
+    ls::RopeParams a;
+    a.q = q;
+    a.sq = q_stride;
+    a.k = k;
+    a.sk = k_stride;
+    a.cos = cos;
+    a.sc = cos_stride;
+    a.sin = sin;
+    a.ss = sin_stride;
+    a.qo = q_out;
+    a.sqo = q_out_stride;
+    a.ko = k_out;
+    a.sko = k_out_stride;
+    a.rows = rows;
+    a.hq = hq;
+    a.hk = hk;
+    a.d = head_dim;
+    return hip_status(ls::launch_rope_qk(a, (hipStream_t)stream), "ls_rope_qk");
+}
+
+int ls_rope_write_decode(const void* qkv, int64_t qkv_stride, const int64_t* positions,
+                         const void* cos, const void* sin, int64_t table_stride, int table_rows,
+                         const int64_t* slots, void* k_pool, void* v_pool,
+                         const int64_t* kv_strides, int num_blocks, int page, void* q_out,
+                         const int64_t* q_strides, void* kmin, void* kmax,
+                         const int64_t* bounds_strides, int batch, int hq, int hk, int head_dim,
+                         void* stream) {
+    if (!qkv || !positions || !cos || !sin || !slots || !k_pool || !v_pool || !kv_strides ||
+        !q_out || !q_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim < 2 || head_dim > 1024 || head_dim % 2 != 0)
+        return fail(LS_ERR_INVALID, "head_dim must be even and in [2, 1024], got %d", head_dim);
+    if (hk < 1 || hq < 1 || hq % hk != 0 || hq + 2 * hk > 65535)
+        return fail(LS_ERR_INVALID, "hq must be a positive multiple of hk (hq %d, hk %d)", hq, hk);
+    if (batch < 0 || batch > 65535) return fail(LS_ERR_INVALID, "batch must be in [0, 65535]");
+    if (table_rows < 1 || num_blocks < 1 || page < 1)
+        return fail(LS_ERR_INVALID, "table_rows, num_blocks and page must be >= 1");
+    if ((kmin == nullptr) != (kmax == nullptr) || (kmin && !bounds_strides))
+        return fail(LS_ERR_INVALID, "kmin, kmax and bounds_strides must be given together");
+    ls::RopeWriteParams a;
+    a.qkv = qkv;
+    a.sqkv = qkv_stride;
+    a.pos = positions;
+    a.cos = cos;
+    a.sin = sin;
+    a.st = table_stride;
+    a.tab_rows = table_rows;
+    a.slots = slots;
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.sp_b = kv_strides[0];
+    a.sp_t = kv_strides[1];
+    a.sp_h = kv_strides[2];
+    a.num_blocks = num_blocks;
+    a.page = page;
+    a.q_out = q_out;
+    a.sq_b = q_strides[0];
+    a.sq_h = q_strides[1];
+    a.sq_r = q_strides[2];
+    a.kmin = kmin;
+    a.kmax = kmax;
+    a.sb_b = kmin ? bounds_strides[0] : 0;
+    a.sb_h = kmin ? bounds_strides[1] : 0;
+    a.B = batch;
+    a.hq = hq;
+    a.hk = hk;
+    a.d = head_dim;
+    return hip_status(ls::launch_rope_write_decode(a, (hipStream_t)stream), "ls_rope_write_decode");
 }
 
 }  // extern "C"

@@ -130,6 +130,15 @@ def _buffers(tag: str, b: int, h: int, splits: int, n_rep: int, device):
     return out, work, cnt
 
 
+def check_out(out: torch.Tensor, q: torch.Tensor) -> torch.Tensor:
+    """A caller's output buffer for q [B, H_kv, n_rep, D]."""
+    if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device \
+            or not _aligned(out, 16):
+        raise ValueError(f"out must be {q.dtype} {tuple(q.shape)} on {q.device} with 16-byte "
+                         "aligned rows")
+    return out
+
+
 def _check_common(q, k_pool, v_pool, block_tables, seq_lens):
     if q.stride(-1) != 1 or k_pool.stride(-1) != 1 or v_pool.stride() != k_pool.stride():
         raise ValueError("the HIP kernel needs unit-stride head dims and matching K/V pools")
@@ -148,11 +157,15 @@ def paged_decode_hip(q, k_pool, v_pool, block_tables, seq_lens, max_seq_len: int
                      num_splits: Optional[int] = None,
                      softmax_scale: Optional[float] = None,
                      k_scale=None, v_scale=None, k_zero=None, v_zero=None,
-                     k_residual=None, res_rows=None) -> torch.Tensor:
+                     k_residual=None, res_rows=None,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Paged decode on the HIP kernels -> [B, H_kv, n_rep, D] (q.dtype).
 
     kernels/cuda/paged_decode_cuda.py:202-252. The returned tensor is a view
-    of a persistent buffer, overwritten by the next call of the same shape.
+    of a persistent buffer, overwritten by the next call of the same shape,
+    or `out` when given ([B, H_kv, n_rep, D] fp16 with 16-byte aligned rows,
+    e.g. a contiguous [B, H_kv * n_rep * D] buffer the output projection
+    reads without a copy).
     """
     reason = ineligible_reason(q, k_pool, k_scale, k_residual, v_scale, k_zero, v_zero, res_rows)
     if reason is not None:
@@ -164,10 +177,11 @@ def paged_decode_hip(q, k_pool, v_pool, block_tables, seq_lens, max_seq_len: int
     splits = max(1, min(MAX_SPLITS, splits))
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
     is_int8 = k_pool.dtype == torch.int8
-    out, work, cnt = _buffers("hip_i8" if is_int8 else "hip", b, h_kv, splits, n_rep, q.device)
+    buf, work, cnt = _buffers("hip_i8" if is_int8 else "hip", b, h_kv, splits, n_rep, q.device)
+    target = buf if out is None else check_out(out, q)
     L = _lib.lib()
     P, S = _lib.ptr, _lib.strides
-    common_tail = (P(out), S(out, 3), P(work), P(cnt), b, h_kv, n_rep, d, k_pool.shape[1],
+    common_tail = (P(target), S(target, 3), P(work), P(cnt), b, h_kv, n_rep, d, k_pool.shape[1],
                    splits, int(max_seq_len), float(scale), _lib.stream_of(q.device))
     if is_int8:
         rc = L.ls_paged_decode_int8(
@@ -183,7 +197,7 @@ def paged_decode_hip(q, k_pool, v_pool, block_tables, seq_lens, max_seq_len: int
             P(block_tables), block_tables.stride(0), block_tables.shape[1], P(seq_lens),
             *common_tail)
         _lib.check(rc, "ls_paged_decode_fp16")
-    return out[:, :, :n_rep]
+    return buf[:, :, :n_rep] if out is None else out
 
 
 def combine_splits_hip(partial_acc: torch.Tensor, partial_m: torch.Tensor,

@@ -182,8 +182,10 @@ def budgets(seq_lens: torch.Tensor, ratio: float, recent: int = 2, page: int = 1
 def sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel,
                   num_splits: Optional[int] = None,
                   softmax_scale: Optional[float] = None,
-                  ratio: Optional[float] = None, recent: int = 2) -> torch.Tensor:
-    """Attention over the pages in `sel` [B, H, K] only -> [B, H, n_rep, D].
+                  ratio: Optional[float] = None, recent: int = 2,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention over the pages in `sel` [B, H, K] only -> [B, H, n_rep, D]
+    (into `out` when given, as paged_decode_hip).
 
     With `ratio`, each sequence attends the first max(recent+1,
     ceil(ratio*pages)) entries of its (score-sorted) list for its current
@@ -202,23 +204,25 @@ def sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel,
     splits = num_splits or pdh.choose_splits(b, h, num_sel, q.device)
     splits = max(1, min(splits, max(1, num_sel), pdh.MAX_SPLITS))
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
-    out, work, cnt = pdh._buffers("sparse", b, h, splits, n_rep, q.device)
+    buf, work, cnt = pdh._buffers("sparse", b, h, splits, n_rep, q.device)
+    target = buf if out is None else pdh.check_out(out, q)
     P, S = _lib.ptr, _lib.strides
     rc = _lib.lib().ls_paged_sparse_fp16(
         P(q), S(q, 3), P(k_pool), P(v_pool), S(k_pool, 3), k_pool.shape[0],
         P(block_tables), block_tables.stride(0), block_tables.shape[1], P(seq_lens),
         P(sel), S(sel, 2), num_sel, 0.0 if ratio is None else float(ratio), int(recent),
-        P(out), S(out, 3), P(work), P(cnt), b, h, n_rep, d, k_pool.shape[1],
+        P(target), S(target, 3), P(work), P(cnt), b, h, n_rep, d, k_pool.shape[1],
         splits, 0, float(scale), _lib.stream_of(q.device))
     _lib.check(rc, "ls_paged_sparse_fp16")
-    return out[:, :, :n_rep]
+    return buf[:, :, :n_rep] if out is None else out
 
 
 def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
                      ratio: float = 0.25, recent: int = 2,
                      num_splits: Optional[int] = None, max_seq_len: Optional[int] = None,
                      softmax_scale: Optional[float] = None,
-                     scoring: str = "bounds") -> torch.Tensor:
+                     scoring: str = "bounds",
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Index, select, attend (two launches). The list width k follows
     `max_seq_len` (the context) when given, else the table's width; each
     sequence then attends its own budget for its current length."""
@@ -231,4 +235,4 @@ def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
     k = budget(ratio, pages, recent)
     sel = index_select(q, kmin, kmax, block_tables, seq_lens, k, ratio, recent)
     return sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel, num_splits,
-                         softmax_scale, ratio=ratio, recent=recent)
+                         softmax_scale, ratio=ratio, recent=recent, out=out)

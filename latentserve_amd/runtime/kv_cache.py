@@ -322,6 +322,15 @@ class PagedKVCache:
             else:
                 self._recompute_bounds(layer_idx)
 
+    def write_slots(self, batch_size: int) -> torch.Tensor:
+        """[batch_size] int64 flat slots (block * page + offset) that advance(1)
+        chose for the active sequences' new token, on the device, at a fixed
+        address (a graph reads them by pointer)."""
+        slots = self._write_slots
+        if slots is None or slots.shape[0] < batch_size or slots.shape[1] != 1:
+            raise RuntimeError("call advance(1, ...) before asking for the write slots")
+        return slots[:batch_size].reshape(batch_size)
+
     def read(self, layer_idx: int, batch_size: int, length: Optional[int] = None):
         """[B, H_kv, L, D] K and V of the active sequences (the gather path,
         paged_cache.py:486-506), on the HIP gather kernel."""

@@ -6,12 +6,13 @@ The reference's model/ stack (model/qwen.py, model/attention/gqa.py) is not
 rebuilt: this is the minimum that gives the decode-attention path its real
 surroundings (28 layers, hidden 1536, 12 query / 2 KV heads, MLP 8960,
 vocab 151936, tied embeddings, RoPE theta 1e6, q/k/v biases) so a captured
-decode step can be timed as BASELINE's configuration 5 asks.  GEMMs and the
-elementwise glue are torch ops (hipBLASLt); the attention is the HIP kernel
-behind the reference's own entry point, reached as GQAAttention.forward's
-decode branch reaches it (model/attention/gqa.py:283-344: q [B, 12, 1, D]
-folded to [B, 2, 6, D], the new K/V written first, then attention over the
-pool).
+decode step can be timed on the reference's full-step configuration.  GEMMs
+are torch (hipBLASLt); everything else is HIP: per layer the fused norms
+(residual add folded in), one launch for RoPE + the K/V store + the query
+fold (GQAAttention.forward's decode branch, model/attention/gqa.py:283-344:
+q [B, 12, 1, D] folded to [B, 2, 6, D], the new K/V written first), the
+paged decode attention writing straight into the output projection's input,
+and SiLU-and-multiply.
 """
 
 from __future__ import annotations
@@ -23,7 +24,9 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
-from latentserve_amd.kernels.gqa import paged_decode as pd
+from latentserve_amd.kernels import fused_elementwise as fe
+from latentserve_amd.kernels.hip import paged_decode_hip as pdh
+from latentserve_amd.kernels.hip import paged_sparse as ps
 from latentserve_amd.runtime.kv_cache import KVCacheSpec, PagedKVCache
 
 
@@ -44,7 +47,9 @@ class DecoderConfig:
 
 
 class Rope:
-    """cos / sin tables to a fixed bound (no rebuild inside a graph)."""
+    """Hugging Face's Qwen2 rotary tables (transformers' Qwen2RotaryEmbedding:
+    fp32 inverse frequencies and angles, cos / sin cast to the model's fp16),
+    built to a fixed bound so that nothing is rebuilt inside a graph."""
 
     def __init__(self, head_dim: int, theta: float, max_seq_len: int, device):
         self.head_dim, self.theta, self.device = head_dim, theta, device
@@ -52,23 +57,13 @@ class Rope:
         self._build_tables(max_seq_len)
 
     def _build_tables(self, n: int) -> None:
-        inv = 1.0 / (self.theta ** (torch.arange(0, self.head_dim, 2, dtype=torch.float64)
+        inv = 1.0 / (self.theta ** (torch.arange(0, self.head_dim, 2, dtype=torch.int64).float()
                                     / self.head_dim))
-        t = torch.arange(n, dtype=torch.float64)
-        freqs = torch.outer(t, inv)
+        freqs = torch.outer(torch.arange(n, dtype=torch.int64).float(), inv)
         emb = torch.cat([freqs, freqs], dim=-1)
-        self.cos = emb.cos().to(torch.float32).to(self.device)
-        self.sin = emb.sin().to(torch.float32).to(self.device)
+        self.cos = emb.cos().to(torch.float16).to(self.device)
+        self.sin = emb.sin().to(torch.float16).to(self.device)
         self.max_seq_len = n
-
-    def apply(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        """x [B, n_heads, 1, D] fp16, pos [B, 1] int64 -> rotated, fp16."""
-        cos = self.cos[pos][:, None]          # [B, 1, 1, D]
-        sin = self.sin[pos][:, None]
-        xf = x.float()
-        half = self.head_dim // 2
-        rot = torch.cat([-xf[..., half:], xf[..., :half]], dim=-1)
-        return (xf * cos + rot * sin).to(x.dtype)
 
 
 class _Attn:
@@ -94,11 +89,6 @@ class _Layer:
         self.w_down = w(h, cfg.intermediate_size)
         self.norm1 = torch.ones(h, dtype=torch.float16, device=device)
         self.norm2 = torch.ones(h, dtype=torch.float16, device=device)
-
-
-def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * w
 
 
 class QwenDecoder:
@@ -146,38 +136,47 @@ class QwenDecoder:
         advanced; `max_position` bounds every position (a graph bucket)."""
         cfg, cache = self.cfg, self.cache
         b = token_ids.shape[0]
-        qd, kvd, hd = cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim, cfg.head_dim
-        n_rep = cfg.num_heads // cfg.num_kv_heads
+        hq, hk, hd = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+        eps = cfg.rms_norm_eps
         tables = cache.block_tables_tensor(b)
         lens = cache.seq_lens_tensor(b)
-        x = F.embedding(token_ids, self.embed)                     # [B, 1, hidden]
+        slots = cache.write_slots(b)
+        pos = positions.reshape(b)
+        q = torch.empty((b, hk, hq // hk, hd), dtype=torch.float16, device=self.device)
+        o = torch.empty_like(q)                                    # = [B, hq * hd], contiguous
+        x = F.embedding(token_ids.reshape(b), self.embed)          # [B, hidden]
+        # The residual is carried into the next norm, which adds and
+        # normalises in one launch (the reference's _run_layers_fused,
+        # model/latentserve_qwen.py:425-450); the last add goes into the
+        # final norm.
+        residual = None
         for li, layer in enumerate(self.layers):
-            h = rms_norm(x, layer.norm1, cfg.rms_norm_eps)
-            qkv = F.linear(h, layer.w_qkv, layer.b_qkv)            # [B, 1, qd + 2 kvd]
-            q = qkv[..., :qd].view(b, 1, cfg.num_heads, hd).transpose(1, 2)
-            k = qkv[..., qd:qd + kvd].view(b, 1, cfg.num_kv_heads, hd).transpose(1, 2)
-            v = qkv[..., qd + kvd:].view(b, 1, cfg.num_kv_heads, hd).transpose(1, 2)
-            q = self.rope.apply(q, positions)
-            k = self.rope.apply(k, positions)
-            cache.write(li, k, v)
-            qg = q.reshape(b, cfg.num_kv_heads, n_rep, hd)          # query head i -> kv head i // 6
-            if self.sparse_ratio is None:
-                o = pd.paged_decode_attention(qg, cache.k_pool[li], cache.v_pool[li], tables, lens,
-                                              num_splits=layer.attn.num_splits,
-                                              softmax_scale=self.scale,
-                                              max_seq_len=max_position + 1)
+            if residual is None:
+                residual = x
+                h = fe.rms_norm(x, layer.norm1, eps)
             else:
-                from latentserve_amd.kernels.hip import paged_sparse as ps
+                h, residual = fe.fused_add_rms_norm(x, residual, layer.norm1, eps)
+            qkv = F.linear(h, layer.w_qkv, layer.b_qkv)            # [B, (hq + 2 hk) hd]
+            kmin = kmax = None
+            if self.sparse_ratio is not None:
                 kmin, kmax = cache.page_bounds(li)
+            # RoPE, the K/V store at this step's slots (and the page bounds)
+            # and q folded to [B, hk, n_rep, hd], in one launch
+            fe.rope_write_decode(qkv, pos, self.rope.cos, self.rope.sin, slots, cache.k_pool[li],
+                                 cache.v_pool[li], hq, hk, q_out=q, kmin=kmin, kmax=kmax)
+            if self.sparse_ratio is None:
+                pdh.paged_decode_hip(q, cache.k_pool[li], cache.v_pool[li], tables, lens,
+                                     max_seq_len=max_position + 1,
+                                     num_splits=layer.attn.num_splits,
+                                     softmax_scale=self.scale, out=o)
+            else:
                 ctx = cache.sparse_context_hint or max_position + 1
-                o = ps.sparse_attention(qg, cache.k_pool[li], cache.v_pool[li], tables, lens,
-                                        kmin, kmax, ratio=self.sparse_ratio,
-                                        recent=layer.attn.sparse_recent, max_seq_len=ctx,
-                                        softmax_scale=self.scale)
-            x = x + F.linear(o.reshape(b, 1, qd), layer.w_o)
-            h = rms_norm(x, layer.norm2, cfg.rms_norm_eps)
-            gu = F.linear(h, layer.w_gate_up)
-            g, u = gu.chunk(2, dim=-1)
-            x = x + F.linear(F.silu(g) * u, layer.w_down)
-        x = rms_norm(x, self.norm, cfg.rms_norm_eps)
-        return F.linear(x, self.lm_head)
+                ps.sparse_attention(q, cache.k_pool[li], cache.v_pool[li], tables, lens, kmin,
+                                    kmax, ratio=self.sparse_ratio,
+                                    recent=layer.attn.sparse_recent, max_seq_len=ctx,
+                                    softmax_scale=self.scale, out=o)
+            x = F.linear(o.view(b, hq * hd), layer.w_o)
+            h, residual = fe.fused_add_rms_norm(x, residual, layer.norm2, eps)
+            x = F.linear(fe.silu_and_mul(F.linear(h, layer.w_gate_up)), layer.w_down)
+        h, _ = fe.fused_add_rms_norm(x, residual, self.norm, eps)
+        return F.linear(h, self.lm_head).view(b, 1, -1)

@@ -27,6 +27,13 @@ How each function is pinned (tests/test_oracle.py):
   and full-budget equality with ``paged_decode``.
 * ``combine`` — the all-empty split case and equality with one-split decode.
 * ``gather`` / ``bounds_update`` — numpy fancy indexing / running min-max.
+* ``rms_norm`` / ``silu_and_mul`` / ``rope`` — Hugging Face's own Qwen2
+  modules (transformers' ``Qwen2RMSNorm``, ``apply_rotary_pos_emb``, the
+  ``silu`` activation) on torch CPU in fp16, plus closed forms (a constant
+  row normalises to the weight; cos 1 / sin 0 is the identity; a quarter
+  turn is rotate_half).
+* ``rope_write_decode`` — ``rope`` per head, the fold q -> [B, H_kv, n_rep,
+  D] by index, the slot rule block * page + offset, and ``bounds_update``.
 """
 
 from __future__ import annotations
@@ -302,3 +309,74 @@ def gather(pool, block_tables, seq_lens, lmax: int):
                         _I64(_st(block_tables)[0]), _ptr(seq_lens), _I32(b), _I32(h), _I32(d),
                         _I32(page), _I32(lmax), _ptr(out))
     return out
+
+
+# ---- fused elementwise ops of the decode step (numpy, fp16 step by step) --
+
+
+def _f16(a):
+    return np.asarray(a, dtype=np.float32).astype(np.float16)
+
+
+def rms_norm(x, w, eps: float, residual=None):
+    """(y, s): s = x, or fp16(residual + x); y = w * fp16(s * rsqrt(mean(s^2)
+    + eps)) with the variance in float64 (kernels/fused_elementwise.py:75-85,
+    Hugging Face's Qwen2RMSNorm: fp32 variance, the normalised value cast to
+    fp16 before the fp16 weight multiply)."""
+    x = np.asarray(x, np.float16)
+    s = x if residual is None else _f16(np.asarray(residual, np.float32) + x.astype(np.float32))
+    h = s.astype(np.float64)
+    inv = 1.0 / np.sqrt((h * h).mean(-1, keepdims=True) + eps)
+    hn = _f16(s.astype(np.float32) * inv.astype(np.float32))
+    y = _f16(np.asarray(w, np.float16).astype(np.float32) * hn.astype(np.float32))
+    return y, s
+
+
+def silu_and_mul(gate_up):
+    """fp16(fp16(silu(g)) * u) over the halves of the last axis
+    (kernels/fused_elementwise.py:88-90: F.silu(gate) * up in fp16)."""
+    gu = np.asarray(gate_up, np.float16)
+    n = gu.shape[-1] // 2
+    g = gu[..., :n].astype(np.float32)
+    with np.errstate(over="ignore"):
+        sg = _f16(g / (np.float32(1) + np.exp(-g)))
+    return _f16(sg.astype(np.float32) * gu[..., n:].astype(np.float32))
+
+
+def rope(x, cos, sin):
+    """fp16(fp16(x * cos) + fp16(rotate_half(x) * sin)) on the last axis
+    (kernels/fused_elementwise.py:93-110, Hugging Face's
+    apply_rotary_pos_emb in fp16); cos / sin broadcast against x."""
+    x = np.asarray(x, np.float16)
+    d = x.shape[-1]
+    rot = np.concatenate([-x[..., d // 2:], x[..., :d // 2]], axis=-1)
+    a = _f16(x.astype(np.float32) * np.asarray(cos, np.float16).astype(np.float32))
+    b = _f16(rot.astype(np.float32) * np.asarray(sin, np.float16).astype(np.float32))
+    return _f16(a.astype(np.float32) + b.astype(np.float32))
+
+
+def rope_write_decode(qkv, positions, cos, sin, slots, k_pool, v_pool, hq: int, hk: int,
+                      kmin=None, kmax=None, page: int = 16):
+    """One decode token per sequence: q_out [B, hk, hq // hk, d] returned;
+    the rotated key and the value stored into k_pool / v_pool [nb, page, hk,
+    d] at flat slots[b] (negative or past the pool: not stored), the page K
+    bounds updated when given.  Positions are clamped into the table."""
+    qkv = np.asarray(qkv, np.float16)
+    b, d = qkv.shape[0], cos.shape[-1]
+    pos = np.clip(np.asarray(positions, np.int64), 0, cos.shape[0] - 1)
+    c, s = cos[pos][:, None, :], sin[pos][:, None, :]
+    q = rope(qkv[:, :hq * d].reshape(b, hq, d), c, s)
+    k = rope(qkv[:, hq * d:(hq + hk) * d].reshape(b, hk, d), c, s)
+    v = qkv[:, (hq + hk) * d:(hq + 2 * hk) * d].reshape(b, hk, d)
+    nb = k_pool.shape[0]
+    stored = []
+    for i in range(b):
+        slot = int(slots[i])
+        if slot < 0 or slot // page >= nb:
+            continue
+        k_pool[slot // page, slot % page] = k[i]
+        v_pool[slot // page, slot % page] = v[i]
+        stored.append(i)
+    if kmin is not None and stored:            # the bounds of the rows stored
+        bounds_update(k[stored], np.asarray(slots, np.int64)[stored], kmin, kmax, page)
+    return q.reshape(b, hk, hq // hk, d)

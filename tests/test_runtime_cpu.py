@@ -97,3 +97,21 @@ def test_capacity_is_enforced_and_rewind_keeps_blocks():
     assert c.tables[0].blocks == blocks
     with pytest.raises(RuntimeError):
         c.advance(1, batch_size=1)          # 33 tokens need a third page: past capacity
+
+
+def test_rope_tables_are_qwen2_rotary_embedding():
+    """The decoder's cos / sin tables are transformers' Qwen2RotaryEmbedding
+    (fp32 angles, cast to fp16) bit for bit."""
+    import pytest
+    qm = pytest.importorskip("transformers.models.qwen2.modeling_qwen2")
+    from transformers import Qwen2Config
+    from latentserve_amd.runtime.qwen_decoder import DecoderConfig, Rope
+
+    c = DecoderConfig()
+    hf = qm.Qwen2RotaryEmbedding(Qwen2Config(
+        hidden_size=c.hidden_size, num_attention_heads=c.num_heads,
+        num_key_value_heads=c.num_kv_heads, rope_theta=c.rope_theta,
+        max_position_embeddings=4096))
+    cos, sin = hf(torch.zeros(1, dtype=torch.float16), torch.arange(4096)[None])
+    r = Rope(c.head_dim, c.rope_theta, 4096, "cpu")
+    assert torch.equal(cos[0], r.cos) and torch.equal(sin[0], r.sin)
