@@ -77,7 +77,9 @@ struct DecodeSmem {
 // Registers of one page for one wave.  K/V as raw dwords; INT8 rows are half
 // as wide and use the low 2 dwords of each slot.
 struct PageBuf {
-    u4 k[4];      // K row `c`, channels 32j+8g..+8   (fp16: 16 B, int8: 8 B)
+    u4 k[4];      // K row `c`: fp16 channels 32j+8g..+8 (16 B each); int8 channels
+                  // 64j+16g..+16 in k[0..1] (16 B each), the fp16 residual's
+                  // the same channels in k[2j], k[2j+1]
     u4 v[4];      // V row 4g+i, channels 8c..8c+8     (fp16: 16 B, int8: 8 B)
     u2 ks;        // INT8: K scales of channels 2*lane, 2*lane+1 (the row is 512 B)
     u2 kz;        // INT8 asym: K zero points, as ks
@@ -116,19 +118,20 @@ __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, i
 #pragma unroll
             for (int i = 0; i < 4; ++i) buf.vz[i] = vzp[(int64_t)i * a.svs_p];
         }
+        // K channels in the INT8 order: lane (c, g) takes 16 contiguous
+        // channels 64j+16g.. of token c per load, so one load instruction
+        // covers 64 bytes of each of 16 token rows (8 bytes a lane would
+        // cover 32 and need twice the cache-line requests per byte, which
+        // caps the walk below the HBM rate)
         if (HAS_RES && buf.res) {
             const half_t* kp = a.k_res + (int64_t)a.res_rows[b] * a.sr_r + (int64_t)c * a.sr_p +
-                               (int64_t)h * a.sr_h + 8 * g;
+                               (int64_t)h * a.sr_h + 16 * g;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) buf.k[j] = *(const u4*)(kp + 32 * j);
+            for (int j = 0; j < 4; ++j) buf.k[j] = *(const u4*)(kp + 64 * (j / 2) + 8 * (j % 2));
         } else {
-            const int8_t* kp = (const int8_t*)a.k_pool + base + (int64_t)c * a.sk_p + 8 * g;
+            const int8_t* kp = (const int8_t*)a.k_pool + base + (int64_t)c * a.sk_p + 16 * g;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const u2 t = stream_load((const u2*)(kp + 32 * j));
-                buf.k[j].x = t.x;
-                buf.k[j].y = t.y;
-            }
+            for (int j = 0; j < 2; ++j) buf.k[j] = stream_load((const u4*)(kp + 64 * j));
             // One coalesced 512-byte row per page, 8 bytes a lane; the
             // compute step spreads it through LDS to the lanes that need
             // each channel (16 lanes share every scale).
@@ -164,6 +167,8 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
             s = mfma16(as_h4(buf.k[j].z, buf.k[j].w), qh[2 * j + 1], s);
         }
     } else {
+        // MFMA step r takes channels 64(r/4) + 16g + 4(r%4) + [0, 4) of the
+        // lane group g (the query is loaded in the same order)
         if (buf.res) {
             // Exact fp16 K from the residual: the unscaled query.
 #pragma unroll
@@ -178,28 +183,24 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
             *(u2*)&kscale[0][2 * lane] = buf.ks;
             if (ASYM) *(u2*)&kscale[1][2 * lane] = buf.kz;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const u2 lo = i8x4_to_h4(buf.k[j].x);
-                const u2 hi = i8x4_to_h4(buf.k[j].y);
-                const f4 ks0 = *(const f4*)&kscale[0][32 * j + 8 * g];
-                const f4 ks1 = *(const f4*)&kscale[0][32 * j + 8 * g + 4];
-                f4 kz0 = {0.f, 0.f, 0.f, 0.f}, kz1 = {0.f, 0.f, 0.f, 0.f};
-                if (ASYM) {
-                    kz0 = *(const f4*)&kscale[1][32 * j + 8 * g];
-                    kz1 = *(const f4*)&kscale[1][32 * j + 8 * g + 4];
-                }
+            for (int r = 0; r < 8; ++r) {
+                const u4 kw = buf.k[r / 4];
+                const uint32_t w = r % 4 == 0 ? kw.x : r % 4 == 1 ? kw.y : r % 4 == 2 ? kw.z : kw.w;
+                const u2 kh = i8x4_to_h4(w);
+                const int ch = 64 * (r / 4) + 16 * g + 4 * (r % 4);
+                const f4 ks = *(const f4*)&kscale[0][ch];
+                f4 kz = {0.f, 0.f, 0.f, 0.f};
+                if (ASYM) kz = *(const f4*)&kscale[1][ch];
                 // q (fp16) x scale (fp32) rounded once to fp16: mixed-precision
                 // multiplies straight from the fp16 query registers
-                h4 q0, q1;
+                h4 qs;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float qa = (float)qh[2 * j][e], qb = (float)qh[2 * j + 1][e];
-                    q0[e] = (half_t)(qa * ks0[e]);
-                    q1[e] = (half_t)(qb * ks1[e]);
-                    if (ASYM) qz += qa * kz0[e] + qb * kz1[e];
+                    const float qa = (float)qh[r][e];
+                    qs[e] = (half_t)(qa * ks[e]);
+                    if (ASYM) qz += qa * kz[e];
                 }
-                s = mfma16(as_h4(lo.x, lo.y), q0, s);
-                s = mfma16(as_h4(hi.x, hi.y), q1, s);
+                s = mfma16(as_h4(kh.x, kh.y), qs, s);
             }
             if (ASYM) qz = group4_sum(qz);
         }
@@ -358,12 +359,21 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
 
 // Diagnostic: the page walk and every load, with the arithmetic replaced by
 // a fold of the loaded words (the loads-only ceiling of the access pattern).
+template <int KIND>
 __device__ __forceinline__ void consume_page(const PageBuf& buf, WaveState& st) {
     uint32_t x = 0;
+    if (KIND == KV_FP16) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) x ^= buf.k[j].x ^ buf.k[j].y ^ buf.k[j].z ^ buf.k[j].w;
+        for (int j = 0; j < 4; ++j) x ^= buf.k[j].x ^ buf.k[j].y ^ buf.k[j].z ^ buf.k[j].w;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x ^= buf.v[i].x ^ buf.v[i].y ^ buf.v[i].z ^ buf.v[i].w;
+        for (int i = 0; i < 4; ++i) x ^= buf.v[i].x ^ buf.v[i].y ^ buf.v[i].z ^ buf.v[i].w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) x ^= buf.k[j].x ^ buf.k[j].y ^ buf.k[j].z ^ buf.k[j].w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x ^= buf.v[i].x ^ buf.v[i].y ^ __builtin_bit_cast(uint32_t, buf.vs[i]);
+        x ^= buf.ks.x ^ buf.ks.y;
+    }
     st.acc[0][0] += __builtin_bit_cast(float, x & 0x3f8fffffu);
     st.m = 0.f;
 }
@@ -576,14 +586,17 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // (The host grid's sequence, which the deal keeps for equal lengths, so
     // the loads need not wait for the deal; reloaded below if it moved.)
     h4 qh[HG][8];
+    // (INT8: the channel order of its K loads, 64(r/4) + 16g + 4(r%4) for
+    // MFMA step r.)
     auto load_q = [&](int bq) {
 #pragma unroll
     for (int hh = 0; hh < HG; ++hh) {
-        const half_t* qp = a.q + (int64_t)bq * a.sq_b + (int64_t)(h0 + hh) * a.sq_h +
-                           (int64_t)(c < a.NR ? c : 0) * a.sq_r + 8 * g;
+        const half_t* qrow = a.q + (int64_t)bq * a.sq_b + (int64_t)(h0 + hh) * a.sq_h +
+                             (int64_t)(c < a.NR ? c : 0) * a.sq_r;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const u4 t = *(const u4*)(qp + 32 * j);
+            const u4 t = KIND == KV_FP16 ? *(const u4*)(qrow + 8 * g + 32 * j)
+                                         : *(const u4*)(qrow + 16 * g + 64 * (j / 2) + 8 * (j % 2));
             qh[hh][2 * j] = as_h4(t.x, t.y);
             qh[hh][2 * j + 1] = as_h4(t.z, t.w);
         }
@@ -814,7 +827,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 for (int hh = 0; hh < HG; ++hh) {
                     if (hds[u] == hh) {
                         if (ABL == 1 || ABL == 2)
-                            consume_page(buf[u], st[hh]);
+                            consume_page<KIND>(buf[u], st[hh]);
                         else
                             compute_page<KIND, ASYM>(buf[u], st[hh], qh[hh], ok_u ? pgs[u] : -1,
                                                      live_len, scale_log2, g, sm.kscale[wv]);
@@ -1012,8 +1025,9 @@ static hipError_t launch_t(const DecodeParams& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// LATENTSERVE_HIP_ABLATION (diagnostic only; the output is meaningless):
-//   loads        the fp16 dense walk with the arithmetic removed
+// LATENTSERVE_HIP_ABLATION (diagnostic only; the output is meaningless), for
+// the fp16 dense walk and the symmetric INT8 walk without a residual:
+//   loads        the walk with the arithmetic removed
 //   loads_noepi  ... and without the wave merge / partials / split merge
 //   noepi        the full arithmetic without the merge stages
 static int ablation() {
@@ -1038,6 +1052,12 @@ static hipError_t launch_kernel(const DecodeParams& a, hipStream_t stream) {
     }
     if (a.kind == KV_FP16) return launch_t<KV_FP16, false, false, false>(a, stream);
     const bool asym = a.k_zero != nullptr, res = a.k_res != nullptr;
+    if (ablation() != 0 && !asym && !res) {
+        const int abl = ablation();
+        if (abl == 1) return launch_t<KV_INT8, false, false, false, 1>(a, stream);
+        if (abl == 2) return launch_t<KV_INT8, false, false, false, 2>(a, stream);
+        return launch_t<KV_INT8, false, false, false, 3>(a, stream);
+    }
     if (asym && res) return launch_t<KV_INT8, true, true, false>(a, stream);
     if (asym) return launch_t<KV_INT8, true, false, false>(a, stream);
     if (res) return launch_t<KV_INT8, false, true, false>(a, stream);
