@@ -53,6 +53,8 @@ namespace ls {
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 
+constexpr int SCALE_ROW = HEAD_DIM + PAGE;
+
 template <int NWT, int HG, bool SCALES>
 struct DecodeSmem {
     // During the walk the merge buffer holds the group's item table: the
@@ -66,8 +68,9 @@ struct DecodeSmem {
     static constexpr int ENT_INTS = 2048 * HG;
     float m[HG][NWT][MAX_NREP];
     float l[HG][NWT][MAX_NREP];
-    // INT8: each wave's K scale (and zero point) row of the page it computes
-    float kscale[SCALES ? NWT : 1][2][HEAD_DIM];
+    // INT8: each wave's K scale (and zero point) row of the page it computes,
+    // then its 16 tokens' V scales (and zero points)
+    float kscale[SCALES ? NWT : 1][2][SCALE_ROW];
     float acc[HG][NWT][MAX_NREP][ROW];
     int ent[ENT_INTS];
     int is_last[HG];
@@ -83,8 +86,8 @@ struct PageBuf {
     u4 v[4];      // V row 4g+i, channels 8c..8c+8     (fp16: 16 B, int8: 8 B)
     u2 ks;        // INT8: K scales of channels 2*lane, 2*lane+1 (the row is 512 B)
     u2 kz;        // INT8 asym: K zero points, as ks
-    float vs[4];  // INT8: V scale of tokens 4g+i
-    float vz[4];  // INT8 asym: V zero points
+    float vs;     // INT8: V scale of token c (the lane group g = 0 covers the page)
+    float vz;     // INT8 asym: V zero point of token c
     int res;      // INT8: this page's K comes from the residual
 };
 
@@ -108,16 +111,11 @@ __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, i
             buf.v[i].x = t.x;
             buf.v[i].y = t.y;
         }
-        const float* vsp = a.v_scale + (int64_t)blk * a.svs_b + (int64_t)(4 * g) * a.svs_p +
-                           (int64_t)h * a.svs_h;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) buf.vs[i] = vsp[(int64_t)i * a.svs_p];
-        if (ASYM) {
-            const float* vzp = a.v_zero + (int64_t)blk * a.svs_b + (int64_t)(4 * g) * a.svs_p +
-                               (int64_t)h * a.svs_h;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) buf.vz[i] = vzp[(int64_t)i * a.svs_p];
-        }
+        // the page's 16 V scales in one load (lanes of token c share an
+        // address), spread to the lanes that need them through LDS
+        const int64_t vso = (int64_t)blk * a.svs_b + (int64_t)c * a.svs_p + (int64_t)h * a.svs_h;
+        buf.vs = a.v_scale[vso];
+        if (ASYM) buf.vz = a.v_zero[vso];
         // K channels in the INT8 order: lane (c, g) takes 16 contiguous
         // channels 64j+16g.. of token c per load, so one load instruction
         // covers 64 bytes of each of 16 token rows (8 bytes a lane would
@@ -156,7 +154,7 @@ struct WaveState {
 template <int KIND, bool ASYM>
 __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, const h4 (&qh)[8],
                                              int page, int len, float scale_log2, int g,
-                                             float (*kscale)[HEAD_DIM]) {
+                                             float (*kscale)[SCALE_ROW]) {
     // ---- S^T = K . Q^T ----
     f4 s = {0.f, 0.f, 0.f, 0.f};
     float qz = 0.f;
@@ -167,6 +165,11 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
             s = mfma16(as_h4(buf.k[j].z, buf.k[j].w), qh[2 * j + 1], s);
         }
     } else {
+        // the page's V scales through the wave's LDS slot (one wave's LDS
+        // accesses stay in order, so the reads below see this page's)
+        const int lane = __lane_id();
+        kscale[0][HEAD_DIM + (lane & 15)] = buf.vs;
+        if (ASYM) kscale[1][HEAD_DIM + (lane & 15)] = buf.vz;
         // MFMA step r takes channels 64(r/4) + 16g + 4(r%4) + [0, 4) of the
         // lane group g (the query is loaded in the same order)
         if (buf.res) {
@@ -177,9 +180,7 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
                 s = mfma16(as_h4(buf.k[j].z, buf.k[j].w), qh[2 * j + 1], s);
             }
         } else {
-            // the wave's scale row through LDS (one wave's accesses stay in
-            // order, so each read sees this page's row)
-            const int lane = __lane_id();
+            // the K scale row through the same slot
             *(u2*)&kscale[0][2 * lane] = buf.ks;
             if (ASYM) *(u2*)&kscale[1][2 * lane] = buf.kz;
 #pragma unroll
@@ -240,11 +241,13 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
 #pragma unroll
         for (int i = 0; i < 4; ++i) pb[i] = (half_t)p[i];
     } else {
+        const f4 vs = *(const f4*)&kscale[0][HEAD_DIM + 4 * g];     // tokens 4g..4g+3
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pb[i] = (half_t)(p[i] * buf.vs[i]);
+        for (int i = 0; i < 4; ++i) pb[i] = (half_t)(p[i] * vs[i]);
         if (ASYM) {
+            const f4 vz = *(const f4*)&kscale[1][HEAD_DIM + 4 * g];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) st.z += p[i] * buf.vz[i];
+            for (int i = 0; i < 4; ++i) st.z += p[i] * vz[i];
         }
     }
     // Rows of V as fp16 pairs: vr[i][kk] = channels (8c+2kk, 8c+2kk+1) of token 4g+i.
@@ -371,7 +374,8 @@ __device__ __forceinline__ void consume_page(const PageBuf& buf, WaveState& st) 
 #pragma unroll
         for (int j = 0; j < 2; ++j) x ^= buf.k[j].x ^ buf.k[j].y ^ buf.k[j].z ^ buf.k[j].w;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x ^= buf.v[i].x ^ buf.v[i].y ^ __builtin_bit_cast(uint32_t, buf.vs[i]);
+        for (int i = 0; i < 4; ++i) x ^= buf.v[i].x ^ buf.v[i].y;
+        x ^= __builtin_bit_cast(uint32_t, buf.vs);
         x ^= buf.ks.x ^ buf.ks.y;
     }
     st.acc[0][0] += __builtin_bit_cast(float, x & 0x3f8fffffu);
