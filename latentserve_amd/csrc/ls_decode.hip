@@ -93,7 +93,7 @@ struct PageBuf {
 
 template <int KIND, bool ASYM, bool HAS_RES>
 __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, int blk, int page,
-                                          int num_pages, int b, int h, int g, int c) {
+                                          int num_pages, int res_row, int h, int g, int c) {
     const int64_t base = (int64_t)blk * a.sk_b + (int64_t)h * a.sk_h;
     if (KIND == KV_FP16) {
         const half_t* kp = (const half_t*)a.k_pool + base + (int64_t)c * a.sk_p + 8 * g;
@@ -122,7 +122,7 @@ __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, i
         // cover 32 and need twice the cache-line requests per byte, which
         // caps the walk below the HBM rate)
         if (HAS_RES && buf.res) {
-            const half_t* kp = a.k_res + (int64_t)a.res_rows[b] * a.sr_r + (int64_t)c * a.sr_p +
+            const half_t* kp = a.k_res + (int64_t)res_row * a.sr_r + (int64_t)c * a.sr_p +
                                (int64_t)h * a.sr_h + 16 * g;
 #pragma unroll
             for (int j = 0; j < 4; ++j) buf.k[j] = *(const u4*)(kp + 64 * (j / 2) + 8 * (j % 2));
@@ -172,6 +172,8 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
         if (ASYM) kscale[1][HEAD_DIM + (lane & 15)] = buf.vz;
         // MFMA step r takes channels 64(r/4) + 16g + 4(r%4) + [0, 4) of the
         // lane group g (the query is loaded in the same order)
+        // (buf.res is the same in every lane: a scalar branch, see the page
+        // loop for why a per-lane one is avoided)
         if (buf.res) {
             // Exact fp16 K from the residual: the unscaled query.
 #pragma unroll
@@ -516,6 +518,14 @@ __device__ GroupWork deal_groups(const DecodeParams& a, int w_id, int lane, int 
     return r;
 }
 
+// s_waitcnt for the vector-memory counter alone (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Claim the next item of the group for the calling wave: an LDS atomic by
 // lane 0.  The result stays in lane 0's register until claimed_item()
 // reads it one iteration later, off the critical path.
@@ -534,6 +544,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // per SIMD.
     constexpr int PF_DEPTH = KIND == KV_FP16 ? 2 : 1;
     constexpr int NB = PF_DEPTH + 1;
+    // Fewest vector-memory instructions one item's load issues (fp16: 4 K +
+    // 4 V; INT8: 4 V + V scale + 2 K + K scale, and the zero points).
+    constexpr int LOADS_PER_PAGE = KIND == KV_FP16 ? 8 : (ASYM ? 10 : 8);
     __shared__ DecodeSmem<NWT, HG, KIND == KV_INT8> sm;
     const int H = a.H;
     // A group serves HG adjacent KV heads of one (sequence, split) with NWT
@@ -615,7 +628,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // An fp16 request needs only a block id that is safe to read: the item is
     // checked against the sequence when it is computed.  (INT8 needs the
     // page to pick its K source, so it checks first.)
-    auto issue_raw = [&](int slot, int it, int blk, int pg, int hh, bool ok, int bseq,
+    auto issue_raw = [&](int slot, int it, int blk, int pg, int hh, bool ok, int rrow,
                          int npages) {
         item[slot] = it;
         blks[slot] = blk;
@@ -623,9 +636,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         hds[slot] = hh;
         if (KIND == KV_FP16) {
             const int safe_blk = (unsigned)blk < (unsigned)a.num_blocks ? blk : 0;
-            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], safe_blk, -1, 0, bseq, h0 + hh, g, c);
+            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], safe_blk, -1, 0, 0, h0 + hh, g, c);
         } else {
-            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], ok ? blk : 0, ok ? pg : -1, npages, bseq,
+            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], ok ? blk : 0, ok ? pg : -1, npages, rrow,
                                            h0 + hh, g, c);
         }
     };
@@ -647,10 +660,14 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     if (b != hb) load_q(b);
     int num_pages = (len + PAGE - 1) / PAGE;
     num_pages = num_pages < a.max_pages ? num_pages : a.max_pages;
+    // the sequence's residual row, read once (the page loads take it as a
+    // value: a load of it per page would make every page request wait)
     bool res_ok = false;
+    int res_row = 0;
     if (HAS_RES) {
         const int rr = a.res_rows[b];
         res_ok = rr >= 0 && rr < a.res_cap;
+        res_row = res_ok ? rr : 0;
     }
 
     // The walk: the sequence's pages (dense) or its selection list (page
@@ -800,7 +817,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                                              : (it < n_items && blk >= 0 && blk < a.num_blocks &&
                                                 pg >= 0 && pg < num_pages &&
                                                 !(HAS_RES && pg == num_pages - 1 && !res_ok));
-            issue_raw(slot, it, blk, pg, hh, ok, b, num_pages);
+            issue_raw(slot, it, blk, pg, hh, ok, res_row, num_pages);
         };
         auto issue = [&](int slot, int it) { issue_with(resolve, slot, it); };
         // The first items are fixed (wave wv takes wv, wv + NWT, ...): their
@@ -814,6 +831,13 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         __syncthreads();
         int it_n = wv + PF_DEPTH * NWT;
         if (item[0] >= n_items) return;
+        // Every load older than the first items' pages is complete here (the
+        // query, table and lengths were needed to get this far), so the loop
+        // is entered with only those pages in flight, as on its back edge.
+        // Said explicitly, the compiler's wait placement sees the same state
+        // on both of the loop's incoming paths instead of waiting on every
+        // trip for loads it cannot prove done.
+        wait_vmcnt<PF_DEPTH * LOADS_PER_PAGE>();
         while (true) {
 #pragma unroll
             for (int u = 0; u < NB; ++u) {
@@ -827,16 +851,24 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 // force conservative waits on the next reuse of its registers
                 const bool ok_u = live(u);
                 const int live_len = ok_u ? len : 0;
-#pragma unroll
-                for (int hh = 0; hh < HG; ++hh) {
-                    if (hds[u] == hh) {
-                        if (ABL == 1 || ABL == 2)
-                            consume_page<KIND>(buf[u], st[hh]);
-                        else
-                            compute_page<KIND, ASYM>(buf[u], st[hh], qh[hh], ok_u ? pgs[u] : -1,
-                                                     live_len, scale_log2, g, sm.kscale[wv]);
-                    }
-                }
+                // Exactly one head's state takes the page, chosen by a
+                // wave-uniform (scalar) branch.  As a per-lane condition the
+                // compiler would mask both computes with skippable regions,
+                // i.e. see a path on which this page's loads are never
+                // waited for, and its wait placement would then hold back
+                // the next request at the top of every trip of the loop.
+                auto take = [&](int hh) {
+                    if (ABL == 1 || ABL == 2)
+                        consume_page<KIND>(buf[u], st[hh]);
+                    else
+                        compute_page<KIND, ASYM>(buf[u], st[hh], qh[hh], ok_u ? pgs[u] : -1,
+                                                 live_len, scale_log2, g, sm.kscale[wv]);
+                };
+                static_assert(HG == 1 || HG == 2, "one or two heads a group");
+                if (HG == 1 || hds[u] == 0)
+                    take(0);
+                else
+                    take(HG - 1);
                 // items arrive in increasing order: past the end, all later are too
                 if (item[(u + 1) % NB] >= n_items) return;
             }
