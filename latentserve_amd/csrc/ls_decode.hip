@@ -172,8 +172,6 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
         if (ASYM) kscale[1][HEAD_DIM + (lane & 15)] = buf.vz;
         // MFMA step r takes channels 64(r/4) + 16g + 4(r%4) + [0, 4) of the
         // lane group g (the query is loaded in the same order)
-        // (buf.res is the same in every lane: a scalar branch, see the page
-        // loop for why a per-lane one is avoided)
         if (buf.res) {
             // Exact fp16 K from the residual: the unscaled query.
 #pragma unroll
@@ -518,14 +516,6 @@ __device__ GroupWork deal_groups(const DecodeParams& a, int w_id, int lane, int 
     return r;
 }
 
-// s_waitcnt for the vector-memory counter alone (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // Claim the next item of the group for the calling wave: an LDS atomic by
 // lane 0.  The result stays in lane 0's register until claimed_item()
 // reads it one iteration later, off the critical path.
@@ -544,9 +534,6 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // per SIMD.
     constexpr int PF_DEPTH = KIND == KV_FP16 ? 2 : 1;
     constexpr int NB = PF_DEPTH + 1;
-    // Fewest vector-memory instructions one item's load issues (fp16: 4 K +
-    // 4 V; INT8: 4 V + V scale + 2 K + K scale, and the zero points).
-    constexpr int LOADS_PER_PAGE = KIND == KV_FP16 ? 8 : (ASYM ? 10 : 8);
     __shared__ DecodeSmem<NWT, HG, KIND == KV_INT8> sm;
     const int H = a.H;
     // A group serves HG adjacent KV heads of one (sequence, split) with NWT
@@ -831,13 +818,6 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         __syncthreads();
         int it_n = wv + PF_DEPTH * NWT;
         if (item[0] >= n_items) return;
-        // Every load older than the first items' pages is complete here (the
-        // query, table and lengths were needed to get this far), so the loop
-        // is entered with only those pages in flight, as on its back edge.
-        // Said explicitly, the compiler's wait placement sees the same state
-        // on both of the loop's incoming paths instead of waiting on every
-        // trip for loads it cannot prove done.
-        wait_vmcnt<PF_DEPTH * LOADS_PER_PAGE>();
         while (true) {
 #pragma unroll
             for (int u = 0; u < NB; ++u) {
@@ -851,12 +831,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 // force conservative waits on the next reuse of its registers
                 const bool ok_u = live(u);
                 const int live_len = ok_u ? len : 0;
-                // Exactly one head's state takes the page, chosen by a
-                // wave-uniform (scalar) branch.  As a per-lane condition the
-                // compiler would mask both computes with skippable regions,
-                // i.e. see a path on which this page's loads are never
-                // waited for, and its wait placement would then hold back
-                // the next request at the top of every trip of the loop.
+                // the page goes to its head's state
                 auto take = [&](int hh) {
                     if (ABL == 1 || ABL == 2)
                         consume_page<KIND>(buf[u], st[hh]);
