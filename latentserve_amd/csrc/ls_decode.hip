@@ -293,6 +293,13 @@ __device__ __forceinline__ void store_coherent(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Sixteen bytes with the same write-through policy (sc1) the compiler gives
+// the relaxed agent-scope store above: one vector store a lane, so a wave
+// writes whole lines instead of four partial passes over them.
+__device__ __forceinline__ void store_coherent4(float* p, f4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
 template <int VEC>
 __device__ void combine_partials(const float* acc, const float* m, const float* l, int S, int NR,
                                  int64_t sa_s, int64_t sa_r, int64_t sm_s, void* out, int out_f32,
@@ -954,8 +961,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 // Device-coherent (write-through) stores: the group that
                 // merges may run on another XCD, whose L2 does not see this
                 // one's.
-#pragma unroll
-                for (int e = 0; e < 4; ++e) store_coherent(pacc + r * HEAD_DIM + d0 + e, at[e]);
+                store_coherent4(pacc + r * HEAD_DIM + d0, at);
                 if (d0 == 0) {
                     store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
                     store_coherent(pl + r, lt);
