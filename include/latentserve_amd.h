@@ -159,12 +159,11 @@ int ls_page_select(const float* scores, const int64_t* score_strides, const int3
                    int batch, int kv_heads, int num_pages, int k, float ratio, int recent,
                    int sorted, int32_t* sel, const int64_t* sel_strides, void* stream);
 
-/* ls_page_scores + ls_page_select (sorted = 0) in one launch: the index and
- * select steps of sparse_attention (kernels/cuda/paged_sparse.py:222-251).
- * counters int32 [B * H_kv], zero before the first call and left zero.
- * scores and its (b, h) strides must be 128-byte aligned (each group of 32
- * pages owns one line); k <= max_pages <= 8192.  With sel == NULL this is
- * ls_page_scores. */
+/* ls_page_scores then ls_page_select (sorted = 0), two launches on the
+ * stream: the index and select steps of sparse_attention
+ * (kernels/cuda/paged_sparse.py:222-251).  counters is unused (may be NULL;
+ * a caller's buffer is left untouched).  k <= max_pages <= 8192.  With
+ * sel == NULL this is ls_page_scores. */
 int ls_sparse_index(const void* q, const int64_t* q_strides, const void* kmin, const void* kmax,
                     const int64_t* bound_strides, int num_blocks, const int32_t* block_tables,
                     int64_t bt_stride, int max_pages, const int32_t* seq_lens, float* scores,

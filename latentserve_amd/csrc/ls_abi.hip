@@ -318,18 +318,14 @@ int ls_sparse_index(const void* q, const int64_t* q_strides, const void* kmin, c
         return fail(LS_ERR_INVALID, "kmin/kmax rows must be 16-byte aligned");
     if (!aligned(scores, 4)) return fail(LS_ERR_INVALID, "scores must be 4-byte aligned");
     const bool fused = sel != nullptr;
+    (void)counters;   // unused since the selection became its own launch
     if (fused) {
-        if (!sel_strides || !counters)
-            return fail(LS_ERR_INVALID, "selection needs sel_strides and counters");
+        if (!sel_strides) return fail(LS_ERR_INVALID, "selection needs sel_strides");
         if (k < 1 || k > max_pages)
             return fail(LS_ERR_INVALID, "k must be in [1, max_pages=%d], got %d", max_pages, k);
         if (max_pages > ls::SELECT_MAX_PAGES)
             return fail(LS_ERR_INVALID, "selection supports max_pages <= %d, got %d",
                         ls::SELECT_MAX_PAGES, max_pages);
-        // each index group's 32 scores must own one 128-byte line
-        if (!rows_aligned(scores, score_strides, 2, 4, 128))
-            return fail(LS_ERR_INVALID,
-                        "with selection, scores and its (b, h) strides must be 128-byte aligned");
     }
     if (batch == 0 || max_pages == 0) return LS_OK;
     ls::IndexParams a;
@@ -353,14 +349,27 @@ int ls_sparse_index(const void* q, const int64_t* q_strides, const void* kmin, c
     a.H = kv_heads;
     a.NR = n_rep;
     a.recent = recent;
-    a.sel = sel;
-    a.sl_b = fused ? sel_strides[0] : 0;
-    a.sl_h = fused ? sel_strides[1] : 0;
-    a.k = k;
-    a.ratio = ratio;
-    a.counters = counters;
-    return hip_status(ls::launch_page_index(a, (hipStream_t)stream),
-                      fused ? "ls_sparse_index" : "ls_page_scores");
+    const int rc = hip_status(ls::launch_page_index(a, (hipStream_t)stream),
+                              fused ? "ls_sparse_index" : "ls_page_scores");
+    if (rc != LS_OK || !fused) return rc;
+    // the selection: one wave a (sequence, head) row, stream-ordered after
+    // the scores it reads
+    ls::SelectParams s;
+    s.scores = scores;
+    s.ss_b = score_strides[0];
+    s.ss_h = score_strides[1];
+    s.seq_lens = seq_lens;
+    s.B = batch;
+    s.H = kv_heads;
+    s.P = max_pages;
+    s.k = k;
+    s.recent = recent;
+    s.sorted = 0;
+    s.ratio = ratio;
+    s.sel = sel;
+    s.sl_b = sel_strides[0];
+    s.sl_h = sel_strides[1];
+    return hip_status(ls::launch_page_select(s, (hipStream_t)stream), "ls_sparse_index");
 }
 
 int ls_page_select(const float* scores, const int64_t* score_strides, const int32_t* seq_lens,

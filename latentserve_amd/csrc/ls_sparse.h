@@ -27,12 +27,6 @@ struct IndexParams {
     float* scores;          // fp32 [B, H, >= max_pages]
     int64_t ss_b, ss_h;
     int B, H, NR, recent;
-    // fused selection (sel != nullptr)
-    int32_t* sel;
-    int64_t sl_b, sl_h;
-    int k;
-    float ratio;
-    int32_t* counters;      // [B * H], zero at rest
 };
 
 struct SelectParams {

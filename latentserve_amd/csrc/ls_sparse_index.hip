@@ -13,17 +13,18 @@
 //    fp16 values is exact in fp32) and reduced over the 16 lanes with four
 //    DPP adds; the page score is the max over the n_rep query heads.  The
 //    work is a pass over 2 x 256 bytes per (page, KV head): HBM-bound.
-//  * Selection: one 256-thread group per (sequence, KV head) holds the row's
-//    keys in registers (32 per thread), finds the n-th largest key by a
-//    4-pass radix select (8-bit digits, LDS histograms), and writes the
-//    selected page ids in page order.  Ties at the threshold are taken in
-//    page order, so the result is deterministic.  With a ratio the first
-//    n_b entries are the sequence's own budget (the rule the sparse decode
-//    kernel applies to the list), the rest of the k entries follow.
-//  * Fused index + select: every index group stores its 32 scores (one
-//    128-byte line) write-through and bumps a per-(sequence, head) arrival
-//    counter; the last group to arrive runs the selection over the row and
-//    resets the counter.  One launch per layer for the selector.
+//  * Selection: a 4-pass radix select (8-bit digits, LDS histograms) finds
+//    the n-th largest key of a (sequence, KV head) row, and the selected
+//    page ids are written in page order.  Ties at the threshold are taken in
+//    page order, so the result is deterministic.  With a ratio the first n_b
+//    entries are the sequence's own budget (the rule the sparse decode kernel
+//    applies to the list), the rest of the k entries follow.  One 256-thread
+//    group a row, the row's keys in its registers (up to 32 a thread).
+//  * sparse_attention's selector is two launches, index then select.  A
+//    single launch in which the last index group of a row ran its selection
+//    was slower than the pair: its arrival count is a device-scope atomic
+//    issued while the other groups stream the page bounds, and such atomics
+//    take several microseconds to return under that traffic.
 #include "ls_common.h"
 #include "ls_sparse.h"
 
@@ -61,10 +62,6 @@ __device__ __forceinline__ void h8_to_f8(u4 x, float* f) {
     }
 }
 
-__device__ __forceinline__ void store_through(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Order-preserving map float -> uint32 (larger float, larger key); -0 and
 // +0 compare equal, as they do for the reference's torch.topk.
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -97,7 +94,6 @@ struct SelectSmem {
     uint32_t hist[2][256];
     uint32_t wsum[4];
     int found[4];
-    int last;
 };
 
 // Inclusive prefix sum over the 256 threads of a group.
@@ -289,9 +285,7 @@ __device__ __attribute__((always_inline)) void select_row(const float* srow, int
         select_row_k<SORTED, 32>(srow, P, n1, n2, out, sm, skeys);
 }
 
-template <bool FUSED>
 __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
-    __shared__ SelectSmem sm;
     const int b = blockIdx.z, h = blockIdx.y;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int c0 = (lane & 15) * 8;
@@ -357,34 +351,8 @@ __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
         if ((lane & 15) == 0 && st[i] != PG_SKIP) {
             const float v = st[i] == PG_SCORE ? best[i]
                             : st[i] == PG_FORCED ? __builtin_inff() : neg_inf();
-            float* dst = a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h + pg[i];
-            if (FUSED)
-                store_through(dst, v);
-            else
-                *dst = v;
+            a.scores[(int64_t)b * a.ss_b + (int64_t)h * a.ss_h + pg[i]] = v;
         }
-    }
-    if constexpr (FUSED) {
-        // scores written through to memory before the arrival is counted
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __syncthreads();
-        const int64_t bh = (int64_t)b * a.H + h;
-        if (threadIdx.x == 0) {
-            const int prev = __hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-            sm.last = prev == (int)gridDim.x - 1;
-        }
-        __syncthreads();
-        if (!sm.last) return;
-        // Every line of the row was written through by its group and none was
-        // read in this launch, so plain loads see the stored scores.
-        const int n1 = budget_pages(L, a.max_pages, a.ratio, a.recent, a.k);
-        select_row<false>(a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h, a.max_pages, n1,
-                          a.k, a.sel + (int64_t)b * a.sl_b + (int64_t)h * a.sl_h, sm, nullptr);
-        if (threadIdx.x == 0)
-            __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -471,20 +439,18 @@ __global__ __launch_bounds__(256) void bounds_rebuild_kernel(BoundsParams a) {
 hipError_t launch_page_index(const IndexParams& p, hipStream_t stream) {
     if (p.B == 0 || p.max_pages == 0) return hipSuccess;
     const dim3 grid((p.max_pages + INDEX_PAGES_PER_GROUP - 1) / INDEX_PAGES_PER_GROUP, p.H, p.B);
-    if (p.sel)
-        hipLaunchKernelGGL(page_index_kernel<true>, grid, dim3(256), 0, stream, p);
-    else
-        hipLaunchKernelGGL(page_index_kernel<false>, grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(page_index_kernel, grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
 hipError_t launch_page_select(const SelectParams& p, hipStream_t stream) {
     if (p.B == 0 || p.k == 0) return hipSuccess;
     const dim3 grid(p.H, p.B);
-    if (p.sorted)
+    if (p.sorted) {
         hipLaunchKernelGGL(page_select_kernel<true>, grid, dim3(256), 0, stream, p);
-    else
-        hipLaunchKernelGGL(page_select_kernel<false>, grid, dim3(256), 0, stream, p);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(page_select_kernel<false>, grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -138,7 +138,7 @@ def select(scores: torch.Tensor, k: int, sorted: bool = False,
 
 def index_select(q, kmin, kmax, block_tables, seq_lens, k: int, ratio: float,
                  recent: int = 2) -> torch.Tensor:
-    """page_scores + select(ratio=...) in one launch -> int32 [B, H, k]."""
+    """page_scores + select(ratio=...) -> int32 [B, H, k] (two launches)."""
     _check_index_inputs(q, kmin, kmax, block_tables, seq_lens)
     b, h, n_rep, d = q.shape
     max_pages = block_tables.shape[1]
@@ -149,11 +149,10 @@ def index_select(q, kmin, kmax, block_tables, seq_lens, k: int, ratio: float,
         raise ValueError(f"k={k} out of range for {max_pages} pages")
     scores = _score_buffer(b, h, max_pages, q.device)
     sel = scratch("sparse_index_sel", (b, h, k), torch.int32, q.device)
-    cnt = scratch("sparse_index_cnt", (b * h,), torch.int32, q.device, init=0)
     P, S = _lib.ptr, _lib.strides
     rc = _lib.lib().ls_sparse_index(
         P(q), S(q, 3), P(kmin), P(kmax), S(kmin, 2), kmin.shape[0], P(block_tables),
-        block_tables.stride(0), max_pages, P(seq_lens), P(scores), S(scores, 2), P(cnt), k,
+        block_tables.stride(0), max_pages, P(seq_lens), P(scores), S(scores, 2), None, k,
         float(ratio), int(recent), P(sel), S(sel, 2), b, h, n_rep, d, PAGE,
         _lib.stream_of(q.device))
     _lib.check(rc, "ls_sparse_index")
