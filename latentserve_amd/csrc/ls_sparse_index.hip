@@ -285,6 +285,9 @@ __device__ __attribute__((always_inline)) void select_row(const float* srow, int
         select_row_k<SORTED, 32>(srow, P, n1, n2, out, sm, skeys);
 }
 
+// NR: query rows per KV head (a compile-time count keeps only those rows'
+// registers, which sets how many index groups a CU holds at once).
+template <int NR>
 __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
     const int b = blockIdx.z, h = blockIdx.y;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -320,10 +323,9 @@ __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
         }
     }
     const half_t* qb = (const half_t*)a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + c0;
-    u4 qv[MAX_NREP];
+    u4 qv[NR];
 #pragma unroll
-    for (int r = 0; r < MAX_NREP; ++r)
-        if (r < a.NR) qv[r] = *(const u4*)(qb + (int64_t)r * a.sq_r);
+    for (int r = 0; r < NR; ++r) qv[r] = *(const u4*)(qb + (int64_t)r * a.sq_r);
 
     float best[2];
 #pragma unroll
@@ -333,16 +335,14 @@ __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
         h8_to_f8(hi[i], hf);
         float bst = neg_inf();
 #pragma unroll
-        for (int r = 0; r < MAX_NREP; ++r) {
-            if (r < a.NR) {                 // uniform over the group
-                float qf[8];
-                h8_to_f8(qv[r], qf);
-                float s = 0.f;
+        for (int r = 0; r < NR; ++r) {
+            float qf[8];
+            h8_to_f8(qv[r], qf);
+            float s = 0.f;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) s += fmaxf(qf[j] * lf[j], qf[j] * hf[j]);
-                s = row16_sum(s);
-                bst = fmaxf(bst, s);
-            }
+            for (int j = 0; j < 8; ++j) s += fmaxf(qf[j] * lf[j], qf[j] * hf[j]);
+            s = row16_sum(s);
+            bst = fmaxf(bst, s);
         }
         best[i] = bst;
     }
@@ -439,7 +439,15 @@ __global__ __launch_bounds__(256) void bounds_rebuild_kernel(BoundsParams a) {
 hipError_t launch_page_index(const IndexParams& p, hipStream_t stream) {
     if (p.B == 0 || p.max_pages == 0) return hipSuccess;
     const dim3 grid((p.max_pages + INDEX_PAGES_PER_GROUP - 1) / INDEX_PAGES_PER_GROUP, p.H, p.B);
-    hipLaunchKernelGGL(page_index_kernel, grid, dim3(256), 0, stream, p);
+    switch (p.NR) {
+#define LS_INDEX_NR(n) \
+    case n: hipLaunchKernelGGL(page_index_kernel<n>, grid, dim3(256), 0, stream, p); break;
+        LS_INDEX_NR(1) LS_INDEX_NR(2) LS_INDEX_NR(3) LS_INDEX_NR(4) LS_INDEX_NR(5) LS_INDEX_NR(6)
+        LS_INDEX_NR(7) LS_INDEX_NR(8) LS_INDEX_NR(9) LS_INDEX_NR(10) LS_INDEX_NR(11)
+        LS_INDEX_NR(12) LS_INDEX_NR(13) LS_INDEX_NR(14) LS_INDEX_NR(15) LS_INDEX_NR(16)
+#undef LS_INDEX_NR
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
