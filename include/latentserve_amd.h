@@ -289,6 +289,26 @@ int ls_rope_write_decode(const void* qkv, int64_t qkv_stride, const int64_t* pos
                          const int64_t* bounds_strides, int batch, int hq, int hk, int head_dim,
                          void* stream);
 
+/* y[M, N] = x[M, K] . w[N, K]^T (+ bias[N]) in fp16 with fp32 sums: the
+ * projections of a decode step (torch Linear weight layout), M <= 64 rows.
+ * Rows of x, w and y are strided (x_stride, w_stride, y_stride elements);
+ * K % 32 == 0 and x, w 16-byte aligned with strides that keep every row so
+ * (y is stored 8 bytes at a time when its alignment allows).  Each output is rounded to fp16
+ * once, after the bias add (after the sum of the partials where K is split
+ * over workgroups: two launches).  Replaces the torch Linear calls of the
+ * reference's decoder layers (model/latentserve_qwen.py, model/fused.py),
+ * which run as cuBLAS GEMMs. */
+int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
+                   const void* bias, void* y, int64_t y_stride, int M, int N, int K,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of device `workspace` ls_decode_gemm needs for these sizes: fp32
+ * partial sums when K is split over workgroups (outputs narrower than 8192
+ * columns), 0 otherwise (workspace may then be NULL).  The contents need no
+ * initial value; calls that share a workspace must be ordered on one
+ * stream.  No counterpart in the reference (a cuBLAS call sizes its own). */
+size_t ls_decode_gemm_workspace_bytes(int M, int N, int K);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,12 +22,13 @@ _I64P = ctypes.POINTER(ctypes.c_int64)
 _I32 = ctypes.c_int
 _F32 = ctypes.c_float
 _I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
 
 LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -75,6 +76,8 @@ _SIGNATURES = {
     "ls_rope_write_decode": [
         _VP, _I64, _VP, _VP, _VP, _I64, _I32, _VP, _VP, _VP, _I64P, _I32, _I32, _VP, _I64P, _VP,
         _VP, _I64P, _I32, _I32, _I32, _I32, _VP],
+    "ls_decode_gemm": [_VP, _I64, _VP, _I64, _VP, _VP, _I64, _I32, _I32, _I32, _VP, _SZ, _VP],
+    "ls_decode_gemm_workspace_bytes": [_I32, _I32, _I32],
     "ls_combine_splits": [
         _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
 }
@@ -103,7 +106,8 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.argtypes = argtypes
             fn.restype = {"ls_last_error": ctypes.c_char_p,
-                          "ls_decode_workspace_bytes": ctypes.c_size_t}.get(name, ctypes.c_int)
+                          "ls_decode_workspace_bytes": ctypes.c_size_t,
+                          "ls_decode_gemm_workspace_bytes": ctypes.c_size_t}.get(name, ctypes.c_int)
         got = handle.ls_abi_version()
         if got != ABI_VERSION:
             raise HipLibraryMissing(

@@ -20,7 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 LIB = os.path.join(PKG, "liblatentserve_hip.so")
 SOURCES = ["ls_abi.hip", "ls_decode.hip", "ls_sparse_index.hip", "ls_int8_write.hip",
-           "ls_gather.hip", "ls_elementwise.hip"]
+           "ls_gather.hip", "ls_elementwise.hip", "ls_gemm.hip"]
 ARCH = os.environ.get("LS_OFFLOAD_ARCH", "gfx950")
 
 # Packed-fp32 VALU forms are disabled for every device pass; fp32 division

@@ -21,6 +21,7 @@
 #include "ls_int8_write.h"
 #include "ls_gather.h"
 #include "ls_elementwise.h"
+#include "ls_gemm.h"
 
 namespace {
 
@@ -133,7 +134,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 6; }
+int ls_abi_version(void) { return 7; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -724,6 +725,49 @@ int ls_rope_write_decode(const void* qkv, int64_t qkv_stride, const int64_t* pos
     a.hk = hk;
     a.d = head_dim;
     return hip_status(ls::launch_rope_write_decode(a, (hipStream_t)stream), "ls_rope_write_decode");
+}
+
+size_t ls_decode_gemm_workspace_bytes(int M, int N, int K) {
+    if (M <= 0 || M > ls::GEMM_MAX_M || N <= 0 || K < 32 || K % 32 != 0) return 0;
+    return ls::decode_gemm_workspace_bytes(M, N, K);
+}
+
+int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
+                   const void* bias, void* y, int64_t y_stride, int M, int N, int K,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+    if (!x || !w || !y) return fail(LS_ERR_INVALID, "null pointer argument");
+    if (M < 0 || M > ls::GEMM_MAX_M || N < 0 || K < 32 || K % 32 != 0)
+        return fail(LS_ERR_INVALID,
+                    "need 0 <= M <= %d, N >= 0, K a positive multiple of 32 (M %d, N %d, K %d)",
+                    ls::GEMM_MAX_M, M, N, K);
+    if (!aligned(x, 16) || !aligned(w, 16) || x_stride % 8 != 0 || w_stride % 8 != 0 ||
+        x_stride < K || w_stride < K)
+        return fail(LS_ERR_INVALID, "x and w rows must be 16-byte aligned and hold K values");
+    if (!aligned(y, 2) || (M > 1 && y_stride < N))
+        return fail(LS_ERR_INVALID, "y must be 2-byte aligned with y_stride >= N");
+    if (bias && !aligned(bias, 2)) return fail(LS_ERR_INVALID, "bias must be 2-byte aligned");
+    ls::GemmParams a;
+    a.x = x;
+    a.ldx = x_stride;
+    a.w = w;
+    a.ldw = w_stride;
+    a.bias = bias;
+    a.y = y;
+    a.ldy = y_stride;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.vec_y = aligned(y, 8) && y_stride % 4 == 0;
+    a.splits = M > 0 && N > 0 ? ls::decode_gemm_splits(M, N, K) : 1;
+    a.part = (float*)workspace;
+    if (a.splits > 1) {
+        const size_t need = ls::decode_gemm_workspace_bytes(M, N, K);
+        if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
+            return fail(LS_ERR_INVALID,
+                        "this product needs a 16-byte aligned workspace of %zu bytes (got %zu)",
+                        need, workspace ? workspace_bytes : (size_t)0);
+    }
+    return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_gemm");
 }
 
 }  // extern "C"

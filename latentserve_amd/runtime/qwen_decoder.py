@@ -6,8 +6,10 @@ The reference's model/ stack (model/qwen.py, model/attention/gqa.py) is not
 rebuilt: this is the minimum that gives the decode-attention path its real
 surroundings (28 layers, hidden 1536, 12 query / 2 KV heads, MLP 8960,
 vocab 151936, tied embeddings, RoPE theta 1e6, q/k/v biases) so a captured
-decode step can be timed on the reference's full-step configuration.  GEMMs
-are torch (hipBLASLt); everything else is HIP: per layer the fused norms
+decode step can be timed on the reference's full-step configuration.  The
+projections run on the HIP weight-streaming GEMM up to 16 rows (hipBLASLt,
+through torch, above that, where it is faster); everything else is HIP as
+well: per layer the fused norms
 (residual add folded in), one launch for RoPE + the K/V store + the query
 fold (GQAAttention.forward's decode branch, model/attention/gqa.py:283-344:
 q [B, 12, 1, D] folded to [B, 2, 6, D], the new K/V written first), the
@@ -24,10 +26,23 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
+from latentserve_amd.kernels import decode_gemm as dg
 from latentserve_amd.kernels import fused_elementwise as fe
 from latentserve_amd.kernels.hip import paged_decode_hip as pdh
 from latentserve_amd.kernels.hip import paged_sparse as ps
 from latentserve_amd.runtime.kv_cache import KVCacheSpec, PagedKVCache
+
+
+# Rows up to which the projections take the HIP GEMM (measured: at 1 and 16
+# rows it streams the weights 1.3-2.7x faster than hipBLASLt; at 64 rows
+# hipBLASLt is faster).
+HIP_GEMM_MAX_ROWS = 16
+
+
+def _linear(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None) -> torch.Tensor:
+    if x.shape[0] <= HIP_GEMM_MAX_ROWS and dg.supports(x, w):
+        return dg.linear(x, w, b)
+    return F.linear(x, w, b)
 
 
 @dataclass
@@ -156,7 +171,7 @@ class QwenDecoder:
                 h = fe.rms_norm(x, layer.norm1, eps)
             else:
                 h, residual = fe.fused_add_rms_norm(x, residual, layer.norm1, eps)
-            qkv = F.linear(h, layer.w_qkv, layer.b_qkv)            # [B, (hq + 2 hk) hd]
+            qkv = _linear(h, layer.w_qkv, layer.b_qkv)            # [B, (hq + 2 hk) hd]
             kmin = kmax = None
             if self.sparse_ratio is not None:
                 kmin, kmax = cache.page_bounds(li)
@@ -175,8 +190,8 @@ class QwenDecoder:
                                     kmax, ratio=self.sparse_ratio,
                                     recent=layer.attn.sparse_recent, max_seq_len=ctx,
                                     softmax_scale=self.scale, out=o)
-            x = F.linear(o.view(b, hq * hd), layer.w_o)
+            x = _linear(o.view(b, hq * hd), layer.w_o)
             h, residual = fe.fused_add_rms_norm(x, residual, layer.norm2, eps)
-            x = F.linear(fe.silu_and_mul(F.linear(h, layer.w_gate_up)), layer.w_down)
+            x = _linear(fe.silu_and_mul(_linear(h, layer.w_gate_up)), layer.w_down)
         h, _ = fe.fused_add_rms_norm(x, residual, self.norm, eps)
-        return F.linear(h, self.lm_head).view(b, 1, -1)
+        return _linear(h, self.lm_head).view(b, 1, -1)

@@ -1,0 +1,97 @@
+"""HIP decode GEMM against an fp32 evaluation of the same product, on an MI355X.
+
+Shapes are the Qwen2.5-1.5B decode projections (qkv 2048 x 1536 with bias,
+o 1536 x 1536, gate_up 17920 x 1536, down 1536 x 8960, lm_head 151936 x
+1536) at 1, 7, 16 and 64 rows, plus ragged widths that end inside a 16-row
+tile and rows that end inside a 16-row column block.  The kernel sums in
+fp32 and rounds once: each output is held to one fp16 step of the
+correctly rounded fp32 result, plus the fp32 summation-order slack.
+"""
+
+from __future__ import annotations
+
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+
+
+def dg():
+    from latentserve_amd.kernels import decode_gemm
+    return decode_gemm
+
+
+def check(y, x, w, b=None):
+    want = x.float() @ w.float().t()
+    if b is not None:
+        want = want + b.float()
+    err = (y.float() - want).abs()
+    # one fp16 rounding (half a step, 2^-11 relative) plus fp32 order slack
+    tol = want.abs() * 2.0**-10 + 1e-3
+    assert (err <= tol).all(), (err.max().item(), (err / tol).max().item())
+
+
+@pytest.mark.parametrize("m", [1, 7, 16, 64])
+@pytest.mark.parametrize("n,k,bias", [(2048, 1536, True), (1536, 1536, False),
+                                      (17920, 1536, False), (1536, 8960, False)])
+def test_qwen_projections(m, n, k, bias):
+    gen = torch.Generator(device="cuda").manual_seed(m * 7 + n + k)
+    x = torch.randn(m, k, device="cuda", generator=gen).half()
+    w = (torch.randn(n, k, device="cuda", generator=gen) * k**-0.5).half()
+    b = torch.randn(n, device="cuda", generator=gen).half() if bias else None
+    y = dg().linear(x, w, b)
+    torch.cuda.synchronize()
+    check(y, x, w, b)
+
+
+@pytest.mark.parametrize("m", [1, 16])
+def test_lm_head(m):
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(m, 1536, device="cuda", generator=gen).half()
+    w = (torch.randn(151936, 1536, device="cuda", generator=gen) * 0.03).half()
+    y = dg().linear(x, w)
+    torch.cuda.synchronize()
+    check(y, x, w)
+    assert torch.equal(y.float().argmax(-1), (x.float() @ w.float().t()).half().float().argmax(-1))
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 100, 64), (17, 37, 96), (33, 5, 32), (50, 8200, 4096),
+                                   (64, 1, 32)])
+def test_ragged_shapes(m, n, k):
+    gen = torch.Generator(device="cuda").manual_seed(m + n + k)
+    x = torch.randn(m, k, device="cuda", generator=gen).half()
+    w = (torch.randn(n, k, device="cuda", generator=gen) * k**-0.5).half()
+    b = torch.randn(n, device="cuda", generator=gen).half()
+    y = dg().linear(x, w, b)
+    torch.cuda.synchronize()
+    check(y, x, w, b)
+
+
+def test_strided_input_and_given_output_and_no_overwrite():
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    big = torch.randn(9, 2048, device="cuda", generator=gen).half()
+    x = big[:, 256:256 + 1536]                     # rows strided by 2048
+    w = (torch.randn(300, 1536, device="cuda", generator=gen) * 0.03).half()
+    out_big = torch.full((9, 320), 7.0, device="cuda", dtype=torch.float16)
+    out = out_big[:, :300]
+    y = dg().linear(x, w, out=out)
+    torch.cuda.synchronize()
+    assert y.data_ptr() == out_big.data_ptr()
+    check(out_big[:, :300], x, w)
+    assert (out_big[:, 300:] == 7).all()          # columns past N untouched
+
+
+def test_zero_rows_and_rejections():
+    w = torch.zeros(16, 64, device="cuda", dtype=torch.float16)
+    assert dg().linear(torch.zeros(0, 64, device="cuda", dtype=torch.float16), w).shape == (0, 16)
+    with pytest.raises(ValueError):
+        dg().linear(torch.zeros(65, 64, device="cuda", dtype=torch.float16), w)
+    with pytest.raises(ValueError):
+        dg().linear(torch.zeros(2, 64, dtype=torch.float16), w.cpu())
+    with pytest.raises(ValueError):                 # K not a multiple of 32
+        dg().linear(torch.zeros(2, 48, device="cuda", dtype=torch.float16),
+                    torch.zeros(16, 48, device="cuda", dtype=torch.float16))
