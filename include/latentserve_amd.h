@@ -289,13 +289,37 @@ int ls_rope_write_decode(const void* qkv, int64_t qkv_stride, const int64_t* pos
                          const int64_t* bounds_strides, int batch, int hq, int hk, int head_dim,
                          void* stream);
 
+/* y[r] = ls_rms_norm of table row ids[r] (int64, clamped into [0,
+ * table_rows)), and rows_out[r] = that table row (NULL to skip): the token
+ * embedding lookup and the first layer's input norm in one launch
+ * (rows_out is the residual the layer carries).  Replaces the reference's
+ * embed_tokens lookup + input_layernorm (model/latentserve_qwen.py decode
+ * loop; the norm as kernels/fused_elementwise.py:194-205). */
+int ls_embed_rms_norm(const void* table, int64_t table_stride, int64_t table_rows,
+                      const int64_t* ids, const void* weight, void* y, int64_t y_stride,
+                      void* rows_out, int64_t rows_out_stride, int rows, int n, float eps,
+                      void* stream);
+
+/* out[r] = index of the largest value of fp16 row x[r, :n] (int64; the
+ * first among equals, NaN above every number): torch.argmax over the last
+ * dimension, the greedy choice of the next token from the logits.  Long
+ * rows are split over workgroups, which need a device workspace of
+ * ls_argmax_workspace_bytes(rows, n) bytes (0: none; else 16-byte aligned,
+ * zero-filled before its first use: its counters are left at zero by each
+ * call; calls sharing it are ordered on one stream).  Replaces
+ * logits.argmax(dim=-1) of the reference's greedy decode loop. */
+size_t ls_argmax_workspace_bytes(int rows, int n);
+int ls_argmax_rows(const void* x, int64_t x_stride, int64_t* out, int rows, int n,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* y[M, N] = x[M, K] . w[N, K]^T (+ bias[N]) in fp16 with fp32 sums: the
  * projections of a decode step (torch Linear weight layout), M <= 64 rows.
  * Rows of x, w and y are strided (x_stride, w_stride, y_stride elements);
  * K % 32 == 0 and x, w 16-byte aligned with strides that keep every row so
  * (y is stored 8 bytes at a time when its alignment allows).  Each output is rounded to fp16
  * once, after the bias add (after the sum of the partials where K is split
- * over workgroups: two launches).  Replaces the torch Linear calls of the
+ * over workgroups: the last workgroup of a tile to finish adds them in split
+ * order).  Replaces the torch Linear calls of the
  * reference's decoder layers (model/latentserve_qwen.py, model/fused.py),
  * which run as cuBLAS GEMMs. */
 int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
@@ -303,11 +327,26 @@ int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_str
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of device `workspace` ls_decode_gemm needs for these sizes: fp32
- * partial sums when K is split over workgroups (outputs narrower than 8192
- * columns), 0 otherwise (workspace may then be NULL).  The contents need no
- * initial value; calls that share a workspace must be ordered on one
- * stream.  No counterpart in the reference (a cuBLAS call sizes its own). */
+ * partial sums and arrival counters when K is split over workgroups (narrow
+ * outputs with long K), 0 otherwise (workspace may then be NULL).  The
+ * workspace is 256-byte aligned and zero-filled before its first use; its
+ * first 64 KiB hold the counters, which each call leaves at zero again.  Calls that share a workspace
+ * must be ordered on one stream.  No counterpart in the reference (a cuBLAS
+ * call sizes its own). */
 size_t ls_decode_gemm_workspace_bytes(int M, int N, int K);
+
+/* y[M, inter] = fp16(fp16(silu(g)) * u) with g = fp16(x . w[:inter]^T +
+ * bias[:inter]) and u = fp16(x . w[inter:]^T + bias[inter:]): the MLP's
+ * gate/up projection (w [2 inter, K], gate rows first) with the activation
+ * in its epilogue, bit-equal to ls_decode_gemm followed by ls_silu_and_mul.
+ * Same operand rules as ls_decode_gemm; refused (LS_ERR_INVALID) for sizes
+ * at which ls_decode_gemm would split K over workgroups
+ * (ls_decode_gemm_workspace_bytes(M, 2 inter, K) != 0).  Replaces the
+ * reference's gate_up projection + silu_and_mul
+ * (kernels/fused_elementwise.py:222-233, model/fused.py). */
+int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
+                           const void* bias, void* y, int64_t y_stride, int M, int inter, int K,
+                           void* stream);
 
 #ifdef __cplusplus
 }

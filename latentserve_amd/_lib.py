@@ -28,7 +28,7 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 7
+ABI_VERSION = 9
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -76,8 +76,13 @@ _SIGNATURES = {
     "ls_rope_write_decode": [
         _VP, _I64, _VP, _VP, _VP, _I64, _I32, _VP, _VP, _VP, _I64P, _I32, _I32, _VP, _I64P, _VP,
         _VP, _I64P, _I32, _I32, _I32, _I32, _VP],
+    "ls_embed_rms_norm": [
+        _VP, _I64, _I64, _VP, _VP, _VP, _I64, _VP, _I64, _I32, _I32, _F32, _VP],
+    "ls_argmax_workspace_bytes": [_I32, _I32],
+    "ls_argmax_rows": [_VP, _I64, _VP, _I32, _I32, _VP, _SZ, _VP],
     "ls_decode_gemm": [_VP, _I64, _VP, _I64, _VP, _VP, _I64, _I32, _I32, _I32, _VP, _SZ, _VP],
     "ls_decode_gemm_workspace_bytes": [_I32, _I32, _I32],
+    "ls_decode_gate_up_silu": [_VP, _I64, _VP, _I64, _VP, _VP, _I64, _I32, _I32, _I32, _VP],
     "ls_combine_splits": [
         _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
 }
@@ -107,7 +112,8 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = argtypes
             fn.restype = {"ls_last_error": ctypes.c_char_p,
                           "ls_decode_workspace_bytes": ctypes.c_size_t,
-                          "ls_decode_gemm_workspace_bytes": ctypes.c_size_t}.get(name, ctypes.c_int)
+                          "ls_decode_gemm_workspace_bytes": ctypes.c_size_t,
+                          "ls_argmax_workspace_bytes": ctypes.c_size_t}.get(name, ctypes.c_int)
         got = handle.ls_abi_version()
         if got != ABI_VERSION:
             raise HipLibraryMissing(

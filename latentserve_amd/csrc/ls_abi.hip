@@ -134,7 +134,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 7; }
+int ls_abi_version(void) { return 9; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -618,6 +618,8 @@ int ls_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t r
     a.sy = y_stride;
     a.res_out = res_out;
     a.sro = res_out_stride;
+    a.ids = nullptr;
+    a.id_rows = 0;
     a.rows = rows;
     a.n = n;
     a.eps = eps;
@@ -626,6 +628,67 @@ int ls_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t r
             (!residual || (aligned(residual, 16) && aligned(res_out, 16) && res_stride % 8 == 0 &&
                            res_out_stride % 8 == 0));
     return hip_status(ls::launch_rms_norm(a, (hipStream_t)stream), "ls_rms_norm");
+}
+
+int ls_embed_rms_norm(const void* table, int64_t table_stride, int64_t table_rows,
+                      const int64_t* ids, const void* weight, void* y, int64_t y_stride,
+                      void* rows_out, int64_t rows_out_stride, int rows, int n, float eps,
+                      void* stream) {
+    if (!table || !ids || !weight || !y) return fail(LS_ERR_INVALID, "null pointer argument");
+    if (rows < 0 || n < 1 || table_rows < 1)
+        return fail(LS_ERR_INVALID, "rows must be >= 0, n >= 1 and the table non-empty");
+    if (!(eps >= 0.f)) return fail(LS_ERR_INVALID, "eps must be >= 0");
+    ls::NormParams a;
+    a.x = table;
+    a.sx = table_stride;
+    a.res = nullptr;
+    a.sr = 0;
+    a.w = weight;
+    a.y = y;
+    a.sy = y_stride;
+    a.res_out = rows_out;
+    a.sro = rows_out_stride;
+    a.ids = ids;
+    a.id_rows = table_rows;
+    a.rows = rows;
+    a.n = n;
+    a.eps = eps;
+    a.vec = n % 8 == 0 && aligned(table, 16) && aligned(weight, 16) && aligned(y, 16) &&
+            table_stride % 8 == 0 && y_stride % 8 == 0 &&
+            (!rows_out || (aligned(rows_out, 16) && rows_out_stride % 8 == 0));
+    return hip_status(ls::launch_rms_norm(a, (hipStream_t)stream), "ls_embed_rms_norm");
+}
+
+size_t ls_argmax_workspace_bytes(int rows, int n) {
+    if (rows <= 0 || n < 1) return 0;
+    return ls::argmax_workspace_bytes(rows, n);
+}
+
+int ls_argmax_rows(const void* x, int64_t x_stride, int64_t* out, int rows, int n,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+    if (!x || !out) return fail(LS_ERR_INVALID, "null pointer argument");
+    if (rows < 0 || rows > 65535 || n < 1)
+        return fail(LS_ERR_INVALID, "rows must be in [0, 65535] and n >= 1");
+    ls::ArgmaxParams a;
+    a.x = x;
+    a.sx = x_stride;
+    a.out = out;
+    a.parts = ls::argmax_parts(n);
+    a.counters = nullptr;
+    a.part_v = nullptr;
+    a.part_i = nullptr;
+    if (a.parts > 1 && rows > 0) {
+        const size_t need = ls::argmax_workspace_bytes(rows, n);
+        if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
+            return fail(LS_ERR_INVALID, "needs a 16-byte aligned workspace of %zu bytes", need);
+        a.counters = (unsigned*)workspace;
+        a.part_v = (float*)(a.counters + rows);
+        a.part_i = (int*)(a.part_v + (size_t)rows * a.parts);
+    }
+    a.rows = rows;
+    a.n = n;
+    a.vec = n % 8 == 0 && aligned(x, 16) && x_stride % 8 == 0;
+    return hip_status(ls::launch_argmax_rows(a, (hipStream_t)stream), "ls_argmax_rows");
 }
 
 int ls_silu_and_mul(const void* gate_up, int64_t gu_stride, void* out, int64_t out_stride,
@@ -760,14 +823,57 @@ int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_str
     a.vec_y = aligned(y, 8) && y_stride % 4 == 0;
     a.splits = M > 0 && N > 0 ? ls::decode_gemm_splits(M, N, K) : 1;
     a.part = (float*)workspace;
+    a.counters = nullptr;
+    a.glu = 0;
     if (a.splits > 1) {
         const size_t need = ls::decode_gemm_workspace_bytes(M, N, K);
-        if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
+        if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
             return fail(LS_ERR_INVALID,
-                        "this product needs a 16-byte aligned workspace of %zu bytes (got %zu)",
+                        "this product needs a 256-byte aligned workspace of %zu bytes (got %zu)",
                         need, workspace ? workspace_bytes : (size_t)0);
+        if (ls::decode_gemm_units(M, N, K) > ls::GEMM_COUNTERS)
+            return fail(LS_ERR_INVALID, "N %d is too wide for a split product", N);
+        a.counters = (unsigned*)workspace;
+        a.part = (float*)((char*)workspace + ls::GEMM_PART_OFFSET);
     }
     return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_gemm");
+}
+
+int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
+                           const void* bias, void* y, int64_t y_stride, int M, int inter, int K,
+                           void* stream) {
+    if (!x || !w || !y) return fail(LS_ERR_INVALID, "null pointer argument");
+    if (M < 0 || M > ls::GEMM_MAX_M || inter < 0 || inter > (1 << 29) || K < 32 || K % 32 != 0)
+        return fail(LS_ERR_INVALID,
+                    "need 0 <= M <= %d, inter >= 0, K a positive multiple of 32 (M %d, inter %d, "
+                    "K %d)", ls::GEMM_MAX_M, M, inter, K);
+    if (!aligned(x, 16) || !aligned(w, 16) || x_stride % 8 != 0 || w_stride % 8 != 0 ||
+        x_stride < K || w_stride < K)
+        return fail(LS_ERR_INVALID, "x and w rows must be 16-byte aligned and hold K values");
+    if (!aligned(y, 2) || (M > 1 && y_stride < inter))
+        return fail(LS_ERR_INVALID, "y must be 2-byte aligned with y_stride >= inter");
+    if (bias && !aligned(bias, 2)) return fail(LS_ERR_INVALID, "bias must be 2-byte aligned");
+    if (M > 0 && inter > 0 && ls::decode_gemm_splits(M, 2 * inter, K) != 1)
+        return fail(LS_ERR_INVALID,
+                    "K %d is too long to fuse at this width: use ls_decode_gemm, then "
+                    "ls_silu_and_mul", K);
+    ls::GemmParams a;
+    a.x = x;
+    a.ldx = x_stride;
+    a.w = w;
+    a.ldw = w_stride;
+    a.bias = bias;
+    a.y = y;
+    a.ldy = y_stride;
+    a.M = M;
+    a.N = 2 * inter;
+    a.K = K;
+    a.vec_y = aligned(y, 8) && y_stride % 4 == 0;
+    a.part = nullptr;
+    a.counters = nullptr;
+    a.splits = 1;
+    a.glu = 1;
+    return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_gate_up_silu");
 }
 
 }  // extern "C"

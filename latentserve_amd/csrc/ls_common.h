@@ -77,4 +77,15 @@ __device__ __forceinline__ T stream_load(const T* p) {
     return __builtin_nontemporal_load(p);
 }
 
+// fp16(fp16(silu(g)) * u): the MLP activation as Hugging Face's fp16
+// computation rounds it (silu in fp32 on the fp16 gate, rounded, then the
+// fp16 product).  One definition serves every kernel that applies it, so
+// their results are bit-equal.
+__device__ __forceinline__ _Float16 silu_mul_h(_Float16 g, _Float16 u) {
+#pragma clang fp contract(off)
+    const float gf = (float)g;
+    const _Float16 sg = (_Float16)(gf / (1.f + expf(-gf)));
+    return (_Float16)((float)sg * (float)u);
+}
+
 }  // namespace ls

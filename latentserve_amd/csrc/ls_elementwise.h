@@ -17,13 +17,34 @@ struct NormParams {
     const void* w;
     void* y;
     int64_t sy;
-    void* res_out;            // written when res is given
+    void* res_out;            // written when res is given; without res, a copy of x
     int64_t sro;
+    const int64_t* ids;       // non-NULL: row r of x is x row ids[r] (a table lookup)
+    int64_t id_rows;          // rows of that table (ids clamped into it)
     int rows;
     int n;
     float eps;
     bool vec;                 // every row 16-byte aligned and n a multiple of 8
 };
+
+// out[r] = the first index of the largest value of x row r (NaN counts as
+// largest), as int64.
+struct ArgmaxParams {
+    const void* x;
+    int64_t sx;
+    int64_t* out;
+    float* part_v;            // [rows][parts] a part's best value and index
+    int* part_i;
+    unsigned* counters;       // [rows] arrivals, zero on entry and on exit
+    int parts;                // workgroups a row is split over (1: no workspace)
+    int rows;
+    int n;
+    bool vec;                 // rows 16-byte aligned and n a multiple of 8
+};
+
+// Workgroups a row of n values is split over, and the workspace that needs.
+int argmax_parts(int n);
+size_t argmax_workspace_bytes(int rows, int n);
 
 // out = fp16(fp16(silu(g)) * u), g = gu[:, :inter], u = gu[:, inter:].
 struct SiluParams {
@@ -88,5 +109,6 @@ hipError_t launch_rms_norm(const NormParams& p, hipStream_t stream);
 hipError_t launch_silu_and_mul(const SiluParams& p, hipStream_t stream);
 hipError_t launch_rope_qk(const RopeParams& p, hipStream_t stream);
 hipError_t launch_rope_write_decode(const RopeWriteParams& p, hipStream_t stream);
+hipError_t launch_argmax_rows(const ArgmaxParams& p, hipStream_t stream);
 
 }  // namespace ls

@@ -78,11 +78,18 @@ constexpr int NORM_MAXV = 4;          // 16-byte vectors a thread keeps: n <= 81
 
 // One row per block; the row's (summed) values stay in registers between
 // the variance and the scaling.
+// x row of output row `row`: itself, or the table row its id names.
+__device__ __forceinline__ int64_t x_row(const NormParams& a, int64_t row) {
+    if (!a.ids) return row;
+    const int64_t id = a.ids[row];
+    return id < 0 ? 0 : id >= a.id_rows ? a.id_rows - 1 : id;
+}
+
 template <bool RES>
 __global__ __launch_bounds__(NORM_THREADS) void rms_norm_vec_kernel(NormParams a) {
     __shared__ float red[NORM_THREADS / WAVE];
     const int64_t row = blockIdx.x;
-    const half_t* x = (const half_t*)a.x + row * a.sx;
+    const half_t* x = (const half_t*)a.x + x_row(a, row) * a.sx;
     const half_t* r = (const half_t*)a.res + row * a.sr;
     half_t* ro = (half_t*)a.res_out + row * a.sro;
     half_t* y = (half_t*)a.y + row * a.sy;
@@ -99,6 +106,8 @@ __global__ __launch_bounds__(NORM_THREADS) void rms_norm_vec_kernel(NormParams a
                 unpack8(*(const u4*)(r + i), rv);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) s[k][e] = hf(f(rv[e]) + f(s[k][e]));
+                *(u4*)(ro + i) = pack8(s[k]);
+            } else if (a.res_out) {
                 *(u4*)(ro + i) = pack8(s[k]);
             }
 #pragma unroll
@@ -126,7 +135,7 @@ template <bool RES>
 __global__ __launch_bounds__(NORM_THREADS) void rms_norm_any_kernel(NormParams a) {
     __shared__ float red[NORM_THREADS / WAVE];
     const int64_t row = blockIdx.x;
-    const half_t* x = (const half_t*)a.x + row * a.sx;
+    const half_t* x = (const half_t*)a.x + x_row(a, row) * a.sx;
     const half_t* r = (const half_t*)a.res + row * a.sr;
     half_t* ro = (half_t*)a.res_out + row * a.sro;
     half_t* y = (half_t*)a.y + row * a.sy;
@@ -136,6 +145,8 @@ __global__ __launch_bounds__(NORM_THREADS) void rms_norm_any_kernel(NormParams a
         half_t v = x[i];
         if (RES) {
             v = hf(f(r[i]) + f(v));
+            ro[i] = v;
+        } else if (a.res_out) {
             ro[i] = v;
         }
         ss += f(v) * f(v);
@@ -149,12 +160,6 @@ __global__ __launch_bounds__(NORM_THREADS) void rms_norm_any_kernel(NormParams a
     }
 }
 
-__device__ __forceinline__ half_t silu_mul1(half_t g, half_t u) {
-    const float gf = f(g);
-    const half_t sg = hf(gf / (1.f + expf(-gf)));
-    return hf(f(sg) * f(u));
-}
-
 __global__ __launch_bounds__(256) void silu_mul_vec_kernel(SiluParams a) {
     const int64_t row = blockIdx.y;
     const int i = (blockIdx.x * 256 + threadIdx.x) * 8;
@@ -164,7 +169,7 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(SiluParams a) {
     unpack8(*(const u4*)(gu + i), g);
     unpack8(*(const u4*)(gu + a.inter + i), u);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = silu_mul1(g[e], u[e]);
+    for (int e = 0; e < 8; ++e) o[e] = silu_mul_h(g[e], u[e]);
     *(u4*)((half_t*)a.out + row * a.so + i) = pack8(o);
 }
 
@@ -173,7 +178,7 @@ __global__ __launch_bounds__(256) void silu_mul_any_kernel(SiluParams a) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= a.inter) return;
     const half_t* gu = (const half_t*)a.gu + row * a.sgu;
-    ((half_t*)a.out)[row * a.so + i] = silu_mul1(gu[i], gu[a.inter + i]);
+    ((half_t*)a.out)[row * a.so + i] = silu_mul_h(gu[i], gu[a.inter + i]);
 }
 
 // grid (rows, hq + hk), d / 2 threads: thread i rotates the pair (i, i + d/2).
@@ -247,7 +252,146 @@ __global__ __launch_bounds__(512) void rope_write_decode_kernel(RopeWriteParams 
     }
 }
 
+constexpr int ARGMAX_THREADS = 1024;
+constexpr int ARGMAX_BATCH = 8;           // 16-byte loads a thread keeps in flight
+
+// (v, i) replaces the best (bv, bi): larger value, NaN above any number,
+// the smaller index among equals (torch.argmax's first occurrence).
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+    const bool vn = v != v, bn = bv != bv;
+    if (vn || bn) return vn && (!bn || i < bi);
+    return v > bv || (v == bv && i < bi);
+}
+
+// Write-through store (the row's last workgroup may run on another XCD).
+__device__ __forceinline__ void store_through(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_through(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block-wide best of (bv, bi), returned to thread 0.
+__device__ __forceinline__ void argmax_block(float& bv, int& bi, float* sv, int* si) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (argmax_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (threadIdx.x % WAVE == 0) {
+        sv[threadIdx.x / WAVE] = bv;
+        si[threadIdx.x / WAVE] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < (int)blockDim.x / WAVE; ++w)
+            if (argmax_better(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+}
+
+// grid (rows, parts): workgroup p scans chunks [p * cpp, (p + 1) * cpp) of
+// its row, each thread its 16-byte chunks in increasing order (batches of
+// loads issued together).  With parts > 1 the part bests go through the
+// workspace and the row's last workgroup to arrive takes the best of them
+// (ties to the smaller index, so arrival order does not matter).
+__global__ __launch_bounds__(ARGMAX_THREADS) void argmax_rows_kernel(ArgmaxParams a) {
+    __shared__ float sv[ARGMAX_THREADS / WAVE];
+    __shared__ int si[ARGMAX_THREADS / WAVE];
+    __shared__ bool last;
+    const int row = blockIdx.x, part = blockIdx.y;
+    const half_t* x = (const half_t*)a.x + (int64_t)row * a.sx;
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    if (a.vec) {
+        const int chunks = a.n / 8, cpp = (chunks + a.parts - 1) / a.parts;
+        const int c_begin = part * cpp, c_end = c_begin + cpp < chunks ? c_begin + cpp : chunks;
+        for (int c0 = c_begin; c0 < c_end; c0 += ARGMAX_THREADS * ARGMAX_BATCH) {
+            u4 v[ARGMAX_BATCH];
+#pragma unroll
+            for (int k = 0; k < ARGMAX_BATCH; ++k) {
+                const int c = c0 + k * ARGMAX_THREADS + threadIdx.x;
+                v[k] = *(const u4*)(x + 8 * (c < c_end ? c : c_begin));
+            }
+#pragma unroll
+            for (int k = 0; k < ARGMAX_BATCH; ++k) {
+                const int c = c0 + k * ARGMAX_THREADS + threadIdx.x;
+                if (c >= c_end) continue;
+                half_t h[8];
+                unpack8(v[k], h);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (argmax_better(f(h[e]), 8 * c + e, bv, bi)) {
+                        bv = f(h[e]);
+                        bi = 8 * c + e;
+                    }
+            }
+        }
+    } else {
+        const int epp = (a.n + a.parts - 1) / a.parts;
+        const int e_begin = part * epp, e_end = e_begin + epp < a.n ? e_begin + epp : a.n;
+        for (int i = e_begin + threadIdx.x; i < e_end; i += ARGMAX_THREADS)
+            if (argmax_better(f(x[i]), i, bv, bi)) {
+                bv = f(x[i]);
+                bi = i;
+            }
+    }
+    argmax_block(bv, bi, sv, si);
+    if (a.parts == 1) {
+        if (threadIdx.x == 0) a.out[row] = bi;
+        return;
+    }
+    if (threadIdx.x == 0) {
+        store_through(a.part_v + (int64_t)row * a.parts + part, bv);
+        store_through(a.part_i + (int64_t)row * a.parts + part, bi);
+        __builtin_amdgcn_s_waitcnt(0);
+        last = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == (unsigned)a.parts - 1;
+    }
+    __syncthreads();
+    if (!last || threadIdx.x != 0) return;
+    // the parts were written through and not read before in this launch
+    for (int p = 0; p < a.parts; ++p) {
+        const float v = a.part_v[(int64_t)row * a.parts + p];
+        const int i = a.part_i[(int64_t)row * a.parts + p];
+        if (p == 0 || argmax_better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    a.out[row] = bi;
+    __hip_atomic_store(a.counters + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
+
+// A part scans at least 4K values: a row of the 151936-word vocabulary
+// takes 38 workgroups.
+constexpr int ARGMAX_PART_VALUES = 4096;
+constexpr int ARGMAX_MAX_PARTS = 64;
+
+int argmax_parts(int n) {
+    const int p = (n + ARGMAX_PART_VALUES - 1) / ARGMAX_PART_VALUES;
+    return p < 1 ? 1 : p > ARGMAX_MAX_PARTS ? ARGMAX_MAX_PARTS : p;
+}
+
+size_t argmax_workspace_bytes(int rows, int n) {
+    const int p = argmax_parts(n);
+    if (p == 1) return 0;
+    return (size_t)rows * (sizeof(unsigned) + (size_t)p * (sizeof(float) + sizeof(int)));
+}
+
+hipError_t launch_argmax_rows(const ArgmaxParams& p, hipStream_t stream) {
+    if (p.rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(p.rows, p.parts), dim3(ARGMAX_THREADS), 0, stream,
+                       p);
+    return hipGetLastError();
+}
 
 hipError_t launch_rms_norm(const NormParams& p, hipStream_t stream) {
     if (p.rows == 0) return hipSuccess;

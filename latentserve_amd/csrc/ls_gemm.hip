@@ -1,5 +1,7 @@
 // Weight-streaming GEMM of the decode step on gfx950:
-//   Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]),  fp16 in and out, fp32 sums.
+//   Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]),  fp16 in and out, fp32 sums,
+// and its gate/up form Y[M, I] = silu(X . Wg^T) * (X . Wu^T) for a weight
+// [Wg; Wu] of 2I rows, the MLP activation applied in the epilogue.
 //
 // At decode batch sizes (M <= 64) every projection of a layer is a pass over
 // its weight matrix: HBM-bound on W (M * K activations stay in L2).  The
@@ -8,19 +10,35 @@
 // 256-CU chip) to 96-128 workgroups.  Here the work unit is a 16-row tile of
 // W (16 output features) and K is split over the waves of a workgroup (the
 // partial tiles summed through LDS) and, where the tiles are too few to fill
-// the chip, over workgroups too: those write fp32 partial sums and a second
-// launch adds them (no atomics: device-scope atomics return slowly while the
-// chip streams).
+// the chip, over workgroups too: those write fp32 partial sums to the
+// workspace and the last workgroup of a tile to finish adds them, in split
+// order, so the result does not depend on which one that is.
+//
+// Each wave takes a K chunk of at most SPW steps of 32 channels as
+// straight-line code: its loads are all issued before the first is used, so
+// the whole chunk is in flight and the compiler's load counting needs no
+// joins (loads under a branch, or issued in a loop after the sums that
+// precede them, made it wait for every load in flight at each step).
+// Chunks shorter than SPW repeat their last step, whose lines are cached,
+// and add zeros for it.  Plain loads: the non-temporal hint measured slower
+// here (4.9 against 5.9 TB/s on the vocabulary projection).
 //
 // MFMA v_mfma_f32_16x16x16f16 with A = 16 rows of W and B = X^T: a lane
-// loads 16 bytes of its W row and 16 bytes of its X row per 32-channel step
-// (64 contiguous bytes of each of 16 rows per load instruction), and the two
+// loads 16 bytes of its W row and 16 bytes of its X row per step (64
+// contiguous bytes of each of 16 rows per load instruction), and the two
 // MFMAs of the step take elements 0-3 and 4-7 of those loads, the channel
 // order of both operands being the same.  Output lane (r, g) holds
 // Y[r][n0 + 4g .. 4g + 3]: one 8-byte store where y's alignment allows.
 //
+// The gate/up form gives a tile 8 gate rows (lanes g = 0, 1 of the output)
+// and the 8 matching up rows (g = 2, 3); the up values cross to the gate
+// lanes with one swizzle, and each output is rounded exactly as the two
+// launches it replaces round it (fp16 gate and up, then the fp16 SiLU
+// product), so the fused and separate paths are bit-equal.
+//
 // The reference runs these projections as torch (cuBLAS) GEMMs inside its
-// model layers (model/fused.py, model/latentserve_qwen.py).
+// model layers (model/fused.py, model/latentserve_qwen.py) and the
+// activation as silu_and_mul (kernels/fused_elementwise.py:222-233).
 #include "ls_common.h"
 #include "ls_gemm.h"
 
@@ -30,23 +48,54 @@ namespace ls {
 
 namespace {
 
-// One workgroup a (16-row tile, split); its blockDim.x / 64 waves take
-// consecutive K chunks of at most SPW steps of 32 channels.  A wave's chunk
-// is straight-line code (plain loads: the non-temporal hint measured slower
-// here, 4.9 against 5.9 TB/s on the vocabulary projection): all its loads
-// issued at once (repeats of the last
-// step where the chunk is shorter than SPW, which re-read cached lines and
-// add zeros), then consumed in order, so the compiler's load counting needs
-// no joins and the whole chunk is in flight.  MB column blocks of 16 rows
-// of X.  The waves' tiles are summed through LDS (blockDim.x / 64 * MB * 1
-// KiB of dynamic shared memory).
-template <int SPW, int TPW, int MB>
+// Device-coherent (write-through, sc1) 16-byte store: the workgroup that
+// sums a tile's partials may run on another XCD, whose L2 does not see this
+// one's.
+__device__ __forceinline__ void store_through4(float* p, f4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// Stores one lane's four outputs y[m][nc .. nc + 3] (fewer at the right
+// edge of a width-n output).
+__device__ __forceinline__ void store_out(const GemmParams& a, int m, int nc, int n,
+                                          const half_t* v) {
+    half_t* yp = (half_t*)a.y + (int64_t)m * a.ldy + nc;
+    if (a.vec_y && nc + 3 < n) {
+        h4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = v[e];
+        *(h4*)yp = o;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (nc + e < n) yp[e] = v[e];
+    }
+}
+
+// W row of output-tile row r: plain tiles hold 16 consecutive rows; gate/up
+// tiles hold gate rows 8T .. 8T + 7 and the up rows I + 8T .. (rows past the
+// edge clamped to a valid one: their outputs are not stored).
+template <bool GLU>
+__device__ __forceinline__ int w_row(const GemmParams& a, int tile, int r) {
+    if (GLU) {
+        const int half_n = a.N / 2, j0 = 8 * tile + (r & 7), j = j0 < half_n ? j0 : half_n - 1;
+        return r < 8 ? j : half_n + j;
+    }
+    const int n = 16 * tile + r;
+    return n < a.N ? n : a.N - 1;
+}
+
+// One workgroup a (TPW tiles, split); its blockDim.x / 64 waves take
+// consecutive K chunks of the split's range.  MB column blocks of 16 rows
+// of X.  The waves' tiles are summed through LDS (blockDim.x / 64 * TPW *
+// MB KiB of dynamic shared memory).
+template <int SPW, int TPW, int MB, bool GLU>
 __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
     extern __shared__ f4 red[];                       // [waves][TPW][MB][WAVE]
     const int nw = blockDim.x / WAVE;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
     const int r = lane & 15, g = lane >> 4;
-    const int n0 = 16 * TPW * blockIdx.x;
+    const int tile0 = TPW * blockIdx.x;
     const int steps = a.K >> 5;
     const int c = blockIdx.y * nw + wv, nc_ = a.splits * nw;   // chunk c of nc_
     const int s0 = (int)((int64_t)steps * c / nc_);
@@ -65,9 +114,8 @@ __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
     u4 xb[SPW][MB];
     u4 wb[2][SPW];
     auto load_w = [&](int b, int t) {
-        // rows past N read a valid row (clamped); their outputs are not stored
-        const int n = n0 + 16 * t + r, nr = n < a.N ? n : a.N - 1;
-        const half_t* wp = (const half_t*)a.w + (int64_t)nr * a.ldw + 32 * s0 + 8 * g;
+        const half_t* wp = (const half_t*)a.w + (int64_t)w_row<GLU>(a, tile0 + t, r) * a.ldw +
+                           32 * s0 + 8 * g;
 #pragma unroll
         for (int i = 0; i < SPW; ++i) {
             const int st = i < last ? i : last;
@@ -123,73 +171,108 @@ __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
                 for (int mb = 0; mb < MB; ++mb)
                     acc[t][mb] += red[((p * TPW + t) * MB + mb) * WAVE + lane];
     }
+    // wave 0 alone from here
+
+    if (GLU) {
+        // splits == 1 (host): lanes g = 0, 1 hold gate columns 8T + 4g + e,
+        // lanes g + 2 the matching up columns
+        const int half_n = a.N / 2;
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-        const int nc = n0 + 16 * t + 4 * g;   // this lane's 4 output columns
-        if (nc >= a.N) continue;
-        if (a.splits > 1) {
-            const int ldp = (a.N + 3) & ~3;
+        for (int t = 0; t < TPW; ++t)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                f4 up;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) up[e] = __shfl_xor(acc[t][mb][e], 32);
+                const int m = 16 * mb + r, j = 8 * (tile0 + t) + 4 * g;
+                if (g >= 2 || m >= a.M || j >= half_n) continue;
+                half_t o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float gv = acc[t][mb][e], uv = up[e];
+                    if (a.bias && j + e < half_n) {
+                        gv += (float)((const half_t*)a.bias)[j + e];
+                        uv += (float)((const half_t*)a.bias)[half_n + j + e];
+                    }
+                    o[e] = silu_mul_h((half_t)gv, (half_t)uv);
+                }
+                store_out(a, m, j, half_n, o);
+            }
+        return;
+    }
+
+    if (a.splits == 1) {
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            const int nc = 16 * (tile0 + t) + 4 * g;   // this lane's 4 output columns
+            if (nc >= a.N) continue;
+            f4 bv = {0.f, 0.f, 0.f, 0.f};
+            if (a.bias) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    bv[e] = nc + e < a.N ? (float)((const half_t*)a.bias)[nc + e] : 0.f;
+            }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int m = 16 * mb + r;
-                if (m < a.M)
-                    *(f4*)(a.part + ((int64_t)blockIdx.y * a.M + m) * ldp + nc) = acc[t][mb];
-            }
-            continue;
-        }
-        f4 bv = {0.f, 0.f, 0.f, 0.f};
-        if (a.bias) {
+                if (m >= a.M) continue;
+                half_t o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                bv[e] = nc + e < a.N ? (float)((const half_t*)a.bias)[nc + e] : 0.f;
+                for (int e = 0; e < 4; ++e) o[e] = (half_t)(acc[t][mb][e] + bv[e]);
+                store_out(a, m, nc, a.N, o);
+            }
         }
+        return;
+    }
+
+    // ---- split K: partials through the workspace, the last group sums ----
+    const int ldp = (a.N + 3) & ~3;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        const int nc = 16 * (tile0 + t) + 4 * g;
+        if (nc >= a.N) continue;
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
             const int m = 16 * mb + r;
-            if (m >= a.M) continue;
-            half_t* yp = (half_t*)a.y + (int64_t)m * a.ldy + nc;
-            if (a.vec_y && nc + 3 < a.N) {
-                h4 o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = (half_t)(acc[t][mb][e] + bv[e]);
-                *(h4*)yp = o;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (nc + e < a.N) yp[e] = (half_t)(acc[t][mb][e] + bv[e]);
-            }
+            if (m < a.M)
+                store_through4(a.part + ((int64_t)blockIdx.y * a.M + m) * ldp + nc, acc[t][mb]);
         }
     }
-}
-
-// y[m][n] = fp16(sum over splits of part[s][m][n] + bias[n]), four columns
-// a thread.
-__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams a) {
-    const int ldp = (a.N + 3) & ~3, q = ldp / 4;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= a.M * q) return;
-    const int m = i / q, nc = 4 * (i % q);
+    // The partials bypass the non-coherent L2 path, so ordering needs only
+    // their completion before the arrival count (no whole-L2 writeback or
+    // invalidate, which a device-scope fence would issue).
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    int prev = 0;
+    if (lane == 0)
+        prev = __hip_atomic_fetch_add(a.counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0);
+    if (prev != a.splits - 1) return;
+    // Every split of these tiles has arrived.  Their partials were written
+    // through to memory and no group has read those lines in this launch,
+    // so plain loads see them.  Unit u = (t, m, q): four columns.
     const int64_t split_stride = (int64_t)a.M * ldp;
-    const float* pp = a.part + (int64_t)m * ldp + nc;
-    f4 t = *(const f4*)pp;
-    for (int s = 1; s < a.splits; ++s) t += *(const f4*)(pp + s * split_stride);
-    half_t* yp = (half_t*)a.y + (int64_t)m * a.ldy + nc;
+    for (int u = lane; u < TPW * a.M * 4; u += WAVE) {
+        const int t = u / (a.M * 4), m = (u / 4) % a.M, q = u % 4;
+        const int nc = 16 * (tile0 + t) + 4 * q;
+        if (nc >= a.N) continue;
+        const float* pp = a.part + (int64_t)m * ldp + nc;
+        f4 s = *(const f4*)pp;
+        for (int sp = 1; sp < a.splits; ++sp) s += *(const f4*)(pp + sp * split_stride);
+        half_t o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-        if (a.bias && nc + e < a.N) t[e] += (float)((const half_t*)a.bias)[nc + e];
-    if (a.vec_y && nc + 3 < a.N) {
-        h4 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (half_t)t[e];
-        *(h4*)yp = o;
-    } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (nc + e < a.N) yp[e] = (half_t)t[e];
+        for (int e = 0; e < 4; ++e) {
+            if (a.bias && nc + e < a.N) s[e] += (float)((const half_t*)a.bias)[nc + e];
+            o[e] = (half_t)s[e];
+        }
+        store_out(a, m, nc, a.N, o);
     }
+    // back to zero for the next launch
+    if (lane == 0)
+        __hip_atomic_store(a.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-
-}  // namespace
 
 // Steps of 32 channels a wave takes at most, per column-block count of X
 // (the chunk's loads live in registers: 4 VGPRs a step and block of X, 8 a
@@ -203,9 +286,11 @@ constexpr int MAX_GROUP_WAVES = 4;
 constexpr int TPW_MIN_WAVES = 2048;
 
 struct GemmShape {
-    int mb, tpw, splits, group_waves;
+    int mb, tpw, splits, group_waves, units;
 };
 
+// The launch shape of an [M, N, K] product (N: weight rows, 2I for the
+// gate/up form, whose tiles cover as many rows).
 GemmShape gemm_shape(int M, int N, int K) {
     GemmShape s;
     s.mb = (M + 15) / 16 <= 1 ? 1 : (M + 15) / 16 <= 2 ? 2 : 4;
@@ -218,10 +303,10 @@ GemmShape gemm_shape(int M, int N, int K) {
         else if ((int64_t)(tiles + 1) / 2 * chunks >= TPW_MIN_WAVES)
             s.tpw = 2;
     }
-    const int units = (tiles + s.tpw - 1) / s.tpw;           // groups of TPW tiles
+    s.units = (tiles + s.tpw - 1) / s.tpw;                   // groups of TPW tiles
     int w = chunks;
     // enough waves on the chip, without splitting K over workgroups for it
-    int spread = (TARGET_WAVES + units - 1) / units;
+    int spread = (TARGET_WAVES + s.units - 1) / s.units;
     if (spread > MAX_GROUP_WAVES) spread = MAX_GROUP_WAVES;
     if (spread > steps) spread = steps;
     if (w < spread) w = spread;
@@ -233,38 +318,51 @@ GemmShape gemm_shape(int M, int N, int K) {
     return s;
 }
 
-int decode_gemm_splits(int M, int N, int K) { return gemm_shape(M, N, K).splits; }
-
-size_t decode_gemm_workspace_bytes(int M, int N, int K) {
-    const int s = decode_gemm_splits(M, N, K);
-    return s > 1 ? (size_t)s * M * ((N + 3) & ~3) * sizeof(float) : 0;
+template <int TPW, int MB, bool GLU>
+void launch_kernel(const GemmParams& p, const GemmShape& sh, hipStream_t stream) {
+    const dim3 grid(sh.units, p.splits), block(WAVE * sh.group_waves);
+    const size_t lds =
+        sh.group_waves > 1 ? (size_t)sh.group_waves * TPW * MB * WAVE * sizeof(f4) : 0;
+    hipLaunchKernelGGL((decode_gemm_kernel<spw_for(MB), TPW, MB, GLU>), grid, block, lds, stream,
+                       p);
 }
 
-template <int TPW, int MB>
-void launch_kernel(const GemmParams& p, const GemmShape& sh, hipStream_t stream) {
-    const dim3 grid((p.N + 16 * TPW - 1) / (16 * TPW), p.splits), block(WAVE * sh.group_waves);
-    const size_t lds = sh.group_waves > 1 ? (size_t)sh.group_waves * TPW * MB * WAVE * sizeof(f4) : 0;
-    hipLaunchKernelGGL((decode_gemm_kernel<spw_for(MB), TPW, MB>), grid, block, lds, stream, p);
+template <bool GLU>
+void launch_any(const GemmParams& p, const GemmShape& sh, hipStream_t stream) {
+    if (sh.mb == 1 && sh.tpw == 4)
+        launch_kernel<4, 1, GLU>(p, sh, stream);
+    else if (sh.mb == 1 && sh.tpw == 2)
+        launch_kernel<2, 1, GLU>(p, sh, stream);
+    else if (sh.mb == 1)
+        launch_kernel<1, 1, GLU>(p, sh, stream);
+    else if (sh.mb == 2)
+        launch_kernel<1, 2, GLU>(p, sh, stream);
+    else
+        launch_kernel<1, 4, GLU>(p, sh, stream);
+}
+
+}  // namespace
+
+int decode_gemm_splits(int M, int N, int K) { return gemm_shape(M, N, K).splits; }
+
+int decode_gemm_units(int M, int N, int K) { return gemm_shape(M, N, K).units; }
+
+size_t decode_gemm_workspace_bytes(int M, int N, int K) {
+    const GemmShape sh = gemm_shape(M, N, K);
+    if (sh.splits == 1) return 0;
+    return GEMM_PART_OFFSET + (size_t)sh.splits * M * ((N + 3) & ~3) * sizeof(float);
 }
 
 hipError_t launch_decode_gemm(const GemmParams& p, hipStream_t stream) {
     if (p.M == 0 || p.N == 0) return hipSuccess;
     const GemmShape sh = gemm_shape(p.M, p.N, p.K);
     if (sh.splits != p.splits || sh.group_waves > MAX_GROUP_WAVES) return hipErrorInvalidValue;
-    if (sh.mb == 1 && sh.tpw == 4)
-        launch_kernel<4, 1>(p, sh, stream);
-    else if (sh.mb == 1 && sh.tpw == 2)
-        launch_kernel<2, 1>(p, sh, stream);
-    else if (sh.mb == 1)
-        launch_kernel<1, 1>(p, sh, stream);
-    else if (sh.mb == 2)
-        launch_kernel<1, 2>(p, sh, stream);
-    else
-        launch_kernel<1, 4>(p, sh, stream);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.splits == 1) return e;
-    const int q = p.M * (((p.N + 3) & ~3) / 4);
-    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((q + 255) / 256), dim3(256), 0, stream, p);
+    if (p.glu) {
+        if (p.splits != 1 || p.N % 2 != 0) return hipErrorInvalidValue;
+        launch_any<true>(p, sh, stream);
+    } else {
+        launch_any<false>(p, sh, stream);
+    }
     return hipGetLastError();
 }
 

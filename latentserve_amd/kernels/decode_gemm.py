@@ -1,5 +1,10 @@
 """Projections of the decode step on the HIP weight-streaming GEMM.
 
+``gate_up_silu(x, weight)`` is the MLP's gate/up projection with
+silu_and_mul (kernels/fused_elementwise.py:222-233) in the GEMM's
+epilogue: one launch, bit-equal to ``linear`` followed by the separate
+activation kernel.
+
 ``linear(x, weight, bias)`` computes what torch.nn.functional.linear does
 for fp16 operands (x [..., K], weight [N, K] as a torch Linear holds it),
 with fp32 sums and one rounding to fp16 after the bias add.  The reference's
@@ -46,7 +51,9 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     if buf is None or buf.numel() < nbytes:
         if buf is not None:
             _RETIRED.append(buf)
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        # zero-filled: the arrival counters start at zero (and calls leave
+        # them so)
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACE[key] = buf
     return buf
 
@@ -92,3 +99,44 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
         torch.cuda.current_stream(x.device).cuda_stream)
     _lib.check(rc, "ls_decode_gemm")
     return y.view(*x.shape[:-1], n)
+
+
+def gate_up_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """silu(x . Wg^T) * (x . Wu^T) for weight = [Wg; Wu] [2I, K]: [..., I].
+
+    One launch where the product needs no split of K over workgroups;
+    otherwise the GEMM and then the activation kernel (still HIP, same
+    rounding)."""
+    from latentserve_amd.kernels import fused_elementwise as fe
+    for name, t in (("x", x), ("weight", weight)):
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be on a GPU (the HIP kernels have no CPU path)")
+        if t.dtype != torch.float16:
+            raise ValueError(f"{name} must be float16, got {t.dtype}")
+    if weight.dim() != 2 or weight.shape[1] != x.shape[-1] or weight.shape[0] % 2:
+        raise ValueError(f"weight must be [2I, {x.shape[-1]}], got {tuple(weight.shape)}")
+    n2, k = weight.shape
+    inter = n2 // 2
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) % 8) or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    if m > MAX_ROWS:
+        raise ValueError(f"at most {MAX_ROWS} rows a call, got {m}")
+    if m and inter and workspace_bytes(m, n2, k):
+        return fe.silu_and_mul(linear(x, weight, bias), out=out)
+    if bias is not None and (bias.shape != (n2,) or bias.dtype != torch.float16
+                             or not bias.is_contiguous()):
+        raise ValueError(f"bias must be contiguous fp16 [{n2}]")
+    y = torch.empty((m, inter), dtype=x.dtype, device=x.device) if out is None \
+        else out.view(m, inter)
+    if m == 0 or inter == 0:
+        return y.view(*x.shape[:-1], inter)
+    rc = _lib.lib().ls_decode_gate_up_silu(
+        x2.data_ptr(), x2.stride(0) if m > 1 else k, weight.data_ptr(), weight.stride(0),
+        None if bias is None else bias.data_ptr(), y.data_ptr(),
+        y.stride(0) if m > 1 else inter, m, inter, k,
+        torch.cuda.current_stream(x.device).cuda_stream)
+    _lib.check(rc, "ls_decode_gate_up_silu")
+    return y.view(*x.shape[:-1], inter)

@@ -9,6 +9,10 @@ as the reference has them.  The dispatching functions run only the HIP
 kernels: a CPU tensor or a missing library raises, nothing falls back to the
 references.
 
+``embed_rms_norm`` is the token embedding lookup and the first layer's
+input norm in one launch; ``argmax_rows`` is torch.argmax over the last
+dimension (the greedy next token).
+
 ``rope_write_decode`` has no single counterpart: it is the decode layer's
 rope_qk (model/attention/gqa.py:251-253), its paged store of the new K/V rows
 (cache/paged_cache.py write, with the page K bounds of :457-460) and the fold
@@ -231,3 +235,69 @@ def rope_write_decode(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Ten
         None if kmax is None else kmax.data_ptr(), bounds, b, hq, hk, d, _stream(qkv))
     _lib.check(rc, "ls_rope_write_decode")
     return q_out
+
+
+def embed_rms_norm(table: torch.Tensor, ids: torch.Tensor, weight: torch.Tensor, eps: float,
+                   out: Optional[torch.Tensor] = None,
+                   rows_out: Optional[torch.Tensor] = None):
+    """(rms_norm(table[ids]), table[ids]) in one launch: ids [B] or [B, 1]
+    int64 (clamped into the table), table [vocab, n] fp16.  The second
+    tensor is the residual the first layer carries."""
+    _fp16_gpu("table", table)
+    _fp16_gpu("weight", weight)
+    if table.dim() != 2 or weight.shape != (table.shape[1],):
+        raise ValueError("table must be [vocab, n] and weight [n]")
+    if not ids.is_cuda:
+        raise ValueError("ids must be on the GPU")
+    ids1 = ids.reshape(-1)
+    if ids1.dtype != torch.int64 or not ids1.is_contiguous():
+        ids1 = ids1.to(torch.int64).contiguous()     # a small copy (any integer ids)
+    b, n = ids1.shape[0], table.shape[1]
+    y = torch.empty((b, n), dtype=table.dtype, device=table.device) if out is None else out
+    r = torch.empty((b, n), dtype=table.dtype, device=table.device) if rows_out is None \
+        else rows_out
+    for name, t in (("out", y), ("rows_out", r)):
+        if t.shape != (b, n) or t.stride(-1) != 1 or t.dtype != table.dtype:
+            raise ValueError(f"{name} must be fp16 [{b}, {n}] with unit last stride")
+    rc = _lib.lib().ls_embed_rms_norm(
+        table.data_ptr(), table.stride(0), table.shape[0], ids1.data_ptr(), weight.data_ptr(),
+        y.data_ptr(), _row_stride(y), r.data_ptr(), _row_stride(r), b, n, float(eps),
+        _stream(table))
+    _lib.check(rc, "ls_embed_rms_norm")
+    return y, r
+
+
+def argmax_rows(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """torch.argmax(x, dim=-1, keepdim=True) for fp16 x [..., n]: int64."""
+    _fp16_gpu("x", x)
+    x2 = _rows(x)
+    rows = x2.shape[0]
+    o = torch.empty((rows,), dtype=torch.int64, device=x.device) if out is None \
+        else out.view(rows)
+    if o.dtype != torch.int64 or not o.is_contiguous():
+        raise ValueError("out must be contiguous int64")
+    need = int(_lib.lib().ls_argmax_workspace_bytes(rows, x2.shape[1]))
+    ws = _workspace(x.device, need) if need else None
+    rc = _lib.lib().ls_argmax_rows(x2.data_ptr(), _row_stride(x2), o.data_ptr(), rows,
+                                   x2.shape[1], None if ws is None else ws.data_ptr(), need,
+                                   _stream(x))
+    _lib.check(rc, "ls_argmax_rows")
+    return o.view(*x.shape[:-1], 1)
+
+
+_WORKSPACE: dict = {}
+_RETIRED: list = []
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The argmax workspace of a device: zero-filled (its counters start at
+    zero and every call leaves them so), grown to the largest call seen;
+    outgrown buffers are kept, so graphs captured with them stay valid."""
+    key = torch.device(device).index
+    buf = _WORKSPACE.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _RETIRED.append(buf)
+        buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _WORKSPACE[key] = buf
+    return buf

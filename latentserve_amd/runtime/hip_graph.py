@@ -31,6 +31,7 @@ from typing import Optional, Sequence
 
 import torch
 
+from latentserve_amd.kernels import fused_elementwise as fe
 from latentserve_amd.runtime.kv_cache import PagedKVCache
 
 DEFAULT_BUCKETS = (1024, 2048, 4096, 8192, 16384, 32768)
@@ -87,7 +88,7 @@ class CapturedDecode:
                                                   max_position=self.bucket_tokens - 1)
         if not self.greedy:
             return logits, None
-        return logits, logits[:, -1, :].argmax(dim=-1, keepdim=True)
+        return logits, fe.argmax_rows(logits[:, -1, :])
 
     def load(self, token_ids: torch.Tensor, positions: torch.Tensor) -> None:
         """Copy this step's inputs into the buffers the graph reads."""
@@ -179,7 +180,7 @@ class GraphedDecoder:
         logits = self.step(token_ids, positions, slots)
         if self._last_graph is not None:
             return self._last_graph.static_next
-        return logits[:, -1, :].argmax(dim=-1, keepdim=True)
+        return fe.argmax_rows(logits[:, -1, :])
 
     @torch.no_grad()
     def step(self, token_ids: torch.Tensor, positions: torch.Tensor,

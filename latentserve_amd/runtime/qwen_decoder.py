@@ -8,13 +8,14 @@ surroundings (28 layers, hidden 1536, 12 query / 2 KV heads, MLP 8960,
 vocab 151936, tied embeddings, RoPE theta 1e6, q/k/v biases) so a captured
 decode step can be timed on the reference's full-step configuration.  The
 projections run on the HIP weight-streaming GEMM up to 16 rows (hipBLASLt,
-through torch, above that, where it is faster); everything else is HIP as
-well: per layer the fused norms
+through torch, above that, where it is faster), the MLP activation in the
+gate/up GEMM's epilogue; everything else is HIP as well: the embedding
+lookup inside the first norm, per layer the fused norms
 (residual add folded in), one launch for RoPE + the K/V store + the query
 fold (GQAAttention.forward's decode branch, model/attention/gqa.py:283-344:
 q [B, 12, 1, D] folded to [B, 2, 6, D], the new K/V written first), the
-paged decode attention writing straight into the output projection's input,
-and SiLU-and-multiply.
+paged decode attention writing straight into the output projection's
+input.
 """
 
 from __future__ import annotations
@@ -43,6 +44,12 @@ def _linear(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None) 
     if x.shape[0] <= HIP_GEMM_MAX_ROWS and dg.supports(x, w):
         return dg.linear(x, w, b)
     return F.linear(x, w, b)
+
+
+def _gate_up_silu(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    if x.shape[0] <= HIP_GEMM_MAX_ROWS and dg.supports(x, w):
+        return dg.gate_up_silu(x, w)                 # SiLU in the GEMM's epilogue
+    return fe.silu_and_mul(F.linear(x, w))
 
 
 @dataclass
@@ -159,17 +166,16 @@ class QwenDecoder:
         pos = positions.reshape(b)
         q = torch.empty((b, hk, hq // hk, hd), dtype=torch.float16, device=self.device)
         o = torch.empty_like(q)                                    # = [B, hq * hd], contiguous
-        x = F.embedding(token_ids.reshape(b), self.embed)          # [B, hidden]
-        # The residual is carried into the next norm, which adds and
-        # normalises in one launch (the reference's _run_layers_fused,
+        # The token embedding lookup and the first norm are one launch; the
+        # residual is carried into the next norm, which adds and normalises
+        # in one launch (the reference's _run_layers_fused,
         # model/latentserve_qwen.py:425-450); the last add goes into the
         # final norm.
-        residual = None
+        h, residual = fe.embed_rms_norm(self.embed, token_ids.reshape(b), self.layers[0].norm1,
+                                        eps)
+        x = None
         for li, layer in enumerate(self.layers):
-            if residual is None:
-                residual = x
-                h = fe.rms_norm(x, layer.norm1, eps)
-            else:
+            if li > 0:
                 h, residual = fe.fused_add_rms_norm(x, residual, layer.norm1, eps)
             qkv = _linear(h, layer.w_qkv, layer.b_qkv)            # [B, (hq + 2 hk) hd]
             kmin = kmax = None
@@ -192,6 +198,6 @@ class QwenDecoder:
                                     softmax_scale=self.scale, out=o)
             x = _linear(o.view(b, hq * hd), layer.w_o)
             h, residual = fe.fused_add_rms_norm(x, residual, layer.norm2, eps)
-            x = _linear(fe.silu_and_mul(_linear(h, layer.w_gate_up)), layer.w_down)
+            x = _linear(_gate_up_silu(h, layer.w_gate_up), layer.w_down)
         h, _ = fe.fused_add_rms_norm(x, residual, self.norm, eps)
         return _linear(h, self.lm_head).view(b, 1, -1)

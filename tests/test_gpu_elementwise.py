@@ -174,3 +174,72 @@ def test_cpu_tensors_raise():
         fe().rms_norm(x, torch.ones(8, dtype=torch.float16), 1e-6)
     with pytest.raises(ValueError):
         fe().silu_and_mul(x)
+
+
+@pytest.mark.parametrize("n", [1536, 100])
+def test_embed_rms_norm_is_the_lookup_then_the_norm(n):
+    rng = np.random.default_rng(n)
+    table = g((rng.standard_normal((50, n)) * 2).astype(np.float16))
+    w = g(rng.standard_normal(n).astype(np.float16))
+    ids = torch.tensor([3, 0, 49, 3, 17], dtype=torch.int64, device="cuda")
+    y, rows = fe().embed_rms_norm(table, ids, w, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(rows, table[ids])
+    assert torch.equal(y, fe().rms_norm(table[ids], w, 1e-6))
+
+
+def test_embed_rms_norm_clamps_ids_into_the_table():
+    table = g(np.arange(4 * 8, dtype=np.float16).reshape(4, 8))
+    w = g(np.ones(8, np.float16))
+    ids = torch.tensor([-5, 9], dtype=torch.int64, device="cuda")
+    _, rows = fe().embed_rms_norm(table, ids, w, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(rows[0], table[0]) and torch.equal(rows[1], table[3])
+
+
+@pytest.mark.parametrize("rows,n", [(16, 151936), (3, 1000), (5, 37), (1, 8)])
+def test_argmax_rows_is_torch_argmax(rows, n):
+    gen = torch.Generator(device="cuda").manual_seed(rows * n)
+    x = torch.randn(rows, n, device="cuda", generator=gen).half()
+    got = fe().argmax_rows(x)
+    torch.cuda.synchronize()
+    assert torch.equal(got, x.argmax(dim=-1, keepdim=True))
+
+
+def test_argmax_rows_ties_nan_inf_and_strided_rows():
+    n = 4096
+    x = torch.zeros(6, n, dtype=torch.float16, device="cuda")
+    x[0] = 1.0                                      # all equal: the first index
+    x[1, 100] = 7.0; x[1, 3000] = 7.0               # a tie: the first of the two
+    x[2] = float("-inf")                            # all -inf: index 0
+    x[3, 2500] = float("nan"); x[3, 10] = float("inf")   # NaN above +inf
+    x[4, 200] = float("nan"); x[4, 100] = float("nan")   # the first NaN
+    x[5, n - 1] = 1.0                               # the last element
+    got = fe().argmax_rows(x)
+    torch.cuda.synchronize()
+    assert got.view(-1).tolist() == [0, 100, 0, 2500, 100, n - 1]
+    assert torch.equal(got, x.argmax(dim=-1, keepdim=True))
+    big = torch.randn(4, n + 64, device="cuda").half()
+    view = big[:, 16:16 + n]                        # rows strided by n + 64
+    assert torch.equal(fe().argmax_rows(view), view.argmax(dim=-1, keepdim=True))
+
+
+def test_argmax_rows_split_rows_repeat_and_replay_in_a_graph():
+    """Rows long enough to be split over workgroups: the last to arrive picks
+    the best part; repeated calls and graph replays (counters left at zero)
+    agree with torch."""
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    x = torch.randn(16, 151936, device="cuda", generator=gen).half()
+    want = x.argmax(dim=-1, keepdim=True)
+    for _ in range(3):
+        assert torch.equal(fe().argmax_rows(x), want)
+    out = torch.empty(16, 1, dtype=torch.int64, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fe().argmax_rows(x, out=out)
+    for i in range(3):
+        x[i, 1000 * i + 7] = 100.0                     # move the maximum between replays
+        want = x.argmax(dim=-1, keepdim=True)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i

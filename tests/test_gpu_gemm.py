@@ -95,3 +95,71 @@ def test_zero_rows_and_rejections():
     with pytest.raises(ValueError):                 # K not a multiple of 32
         dg().linear(torch.zeros(2, 48, device="cuda", dtype=torch.float16),
                     torch.zeros(16, 48, device="cuda", dtype=torch.float16))
+
+
+def fe():
+    from latentserve_amd.kernels import fused_elementwise
+    return fused_elementwise
+
+
+@pytest.mark.parametrize("m", [1, 7, 16])
+@pytest.mark.parametrize("inter,k,bias", [(8960, 1536, False), (100, 64, True), (36, 96, False),
+                                          (1000, 4096, True)])
+def test_gate_up_silu_is_the_gemm_then_the_activation_bit_for_bit(m, inter, k, bias):
+    gen = torch.Generator(device="cuda").manual_seed(m + inter + k)
+    x = torch.randn(m, k, device="cuda", generator=gen).half()
+    w = (torch.randn(2 * inter, k, device="cuda", generator=gen) * k**-0.5 * 2).half()
+    b = torch.randn(2 * inter, device="cuda", generator=gen).half() if bias else None
+    fused = dg().gate_up_silu(x, w, b)
+    two = fe().silu_and_mul(dg().linear(x, w, b))
+    torch.cuda.synchronize()
+    assert fused.shape == (m, inter)
+    assert torch.equal(fused, two)
+    # and within the activation's fp16 rounding of an fp32 evaluation
+    gu = x.float() @ w.float().t() + (b.float() if bias else 0)
+    want = torch.nn.functional.silu(gu[:, :inter]) * gu[:, inter:]
+    assert ((fused.float() - want).abs() <= want.abs() * 2.0**-8 + 2e-3).all()
+
+
+def test_gate_up_silu_too_long_k_takes_two_launches():
+    # K long enough at this width that the product splits over workgroups
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(4, 8960, device="cuda", generator=gen).half()
+    w = (torch.randn(2 * 200, 8960, device="cuda", generator=gen) * 0.01).half()
+    assert dg().workspace_bytes(4, 400, 8960) > 0
+    y = dg().gate_up_silu(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(y, fe().silu_and_mul(dg().linear(x, w)))
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 1536, 8960), (3, 37, 8960), (64, 200, 4096)])
+def test_split_products_repeat_exactly(m, n, k):
+    """K split over workgroups: partials summed by the last group to arrive,
+    in split order, so repeated calls agree bit for bit (and the arrival
+    counters were left at zero, or the second call would not sum)."""
+    assert dg().workspace_bytes(m, n, k) > 0
+    gen = torch.Generator(device="cuda").manual_seed(m * n)
+    x = torch.randn(m, k, device="cuda", generator=gen).half()
+    w = (torch.randn(n, k, device="cuda", generator=gen) * k**-0.5).half()
+    b = torch.randn(n, device="cuda", generator=gen).half()
+    ys = [dg().linear(x, w, b) for _ in range(4)]
+    torch.cuda.synchronize()
+    check(ys[0], x, w, b)
+    assert all(torch.equal(ys[0], y) for y in ys[1:])
+
+
+def test_split_product_in_a_graph_replays_exactly():
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    x = torch.randn(16, 8960, device="cuda", generator=gen).half()
+    w = (torch.randn(1536, 8960, device="cuda", generator=gen) * 0.01).half()
+    want = dg().linear(x, w)
+    out = torch.empty_like(want)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        dg().linear(x, w, out=out)
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
+        dg().linear(x, w)                          # eager work between replays
