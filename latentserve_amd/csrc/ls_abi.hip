@@ -876,4 +876,12 @@ int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64
     return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_gate_up_silu");
 }
 
+int ls_compute_probe(int mode, int groups, int items, float scale, float* out, void* stream) {
+    if (!out) return fail(LS_ERR_INVALID, "null pointer argument");
+    if ((mode != 0 && mode != 1) || groups < 1 || groups > 65535 || items < 1)
+        return fail(LS_ERR_INVALID, "mode 0 or 1, groups in [1, 65535], items >= 1");
+    return hip_status(ls::launch_compute_probe(mode, groups, items, scale, out, (hipStream_t)stream),
+                      "ls_compute_probe");
+}
+
 }  // extern "C"

@@ -1095,4 +1095,184 @@ hipError_t launch_combine(const CombineParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// ---- compute probe: the page compute alone, MFMA against VALU ----
+//
+// Measurement only (no counterpart in the reference).  Every wave applies
+// one page (16 tokens, one KV head, 6 query rows, D = 128) `items` times to
+// its running (m, l, O) state, from registers: no memory traffic, so the
+// kernel's duration is the compute cost of a page.  MODE 0 is the decode
+// kernel's own compute_page (QK and PV on v_mfma_f32_16x16x16f16); MODE 1 is
+// a VALU formulation of the same page given every advantage: the query rows
+// held in registers for the lane's channels, QK as v_dot2_f32_f16 over the
+// lane's 32 channels of one token and a 4-lane sum, the softmax on 16-lane
+// DPP rotations, PV with V in its natural channel-pair layout (lane l owns
+// channels 2l, 2l + 1 of all 16 tokens) and the weights broadcast from
+// registers.  Both write O = acc / l of each wave's 6 rows.
+namespace {
+
+constexpr int PROBE_ROWS = 6;
+constexpr int PROBE_WAVES = 8;
+
+// Synthetic page and query values, exact in fp16.
+__device__ __forceinline__ half_t probe_k(int t, int ch) { return (half_t)(((t * 7 + ch * 3) % 17 - 8) * 0.0625f); }
+__device__ __forceinline__ half_t probe_v(int t, int ch) { return (half_t)(((t * 5 + ch * 11) % 13 - 6) * 0.125f); }
+__device__ __forceinline__ half_t probe_q(int r, int ch) { return (half_t)(((r * 13 + ch * 5) % 11 - 5) * 0.125f); }
+
+__device__ __forceinline__ uint32_t pack_h2(half_t lo, half_t hi) {
+    h2 t = {lo, hi};
+    return __builtin_bit_cast(uint32_t, t);
+}
+
+// Opaque to the optimiser: the page is "new" every item (nothing hoisted).
+template <typename T>
+__device__ __forceinline__ void opaque(T& v) {
+    asm volatile("" : "+v"(v));
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+    // rotations within each 16-lane row: every lane ends with the row's max
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false)));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xf, 0xf, false));
+    return v;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(WAVE * PROBE_WAVES) void compute_probe_kernel(int items, float scale_log2, float* out) {
+    const int lane = threadIdx.x % WAVE, c = lane & 15, g = lane >> 4;
+    const int64_t w = (int64_t)blockIdx.x * PROBE_WAVES + threadIdx.x / WAVE;
+    float* o = out + w * PROBE_ROWS * HEAD_DIM;
+    if (MODE == 0) {
+        PageBuf buf;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t d[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                d[e] = pack_h2(probe_k(c, 32 * j + 8 * g + 2 * e), probe_k(c, 32 * j + 8 * g + 2 * e + 1));
+            buf.k[j] = (u4){d[0], d[1], d[2], d[3]};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t d[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                d[e] = pack_h2(probe_v(4 * g + i, 8 * c + 2 * e), probe_v(4 * g + i, 8 * c + 2 * e + 1));
+            buf.v[i] = (u4){d[0], d[1], d[2], d[3]};
+        }
+        h4 qh[8];
+        const int qr = c < PROBE_ROWS ? c : 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qh[2 * j][e] = probe_q(qr, 32 * j + 8 * g + e);
+                qh[2 * j + 1][e] = probe_q(qr, 32 * j + 8 * g + 4 + e);
+            }
+        WaveState st;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) st.acc[t] = (f4){0.f, 0.f, 0.f, 0.f};
+        st.m = neg_inf();
+        st.l = 0.f;
+        st.z = 0.f;
+        for (int it = 0; it < items; ++it) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                opaque(buf.k[j]);
+                opaque(buf.v[j]);
+            }
+            compute_page<KV_FP16, false>(buf, st, qh, 0, PAGE, scale_log2, g, nullptr);
+        }
+        const float l = group4_sum(st.l);
+        if (c < PROBE_ROWS)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[c * HEAD_DIM + 32 * g + 8 * i + jj] = st.acc[jj][i] / l;
+    } else {
+        // K: lane (token c, group g) holds channels 32j + 8g + [0, 8); the
+        // query rows the same channels; V: lane holds channels 2 lane, 2 lane + 1
+        uint32_t kk[16], qq[PROBE_ROWS][16], vv[PAGE];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int ch = 32 * j + 8 * g + 2 * e;
+                kk[4 * j + e] = pack_h2(probe_k(c, ch), probe_k(c, ch + 1));
+#pragma unroll
+                for (int r = 0; r < PROBE_ROWS; ++r)
+                    qq[r][4 * j + e] = pack_h2(probe_q(r, ch), probe_q(r, ch + 1));
+            }
+#pragma unroll
+        for (int t = 0; t < PAGE; ++t) vv[t] = pack_h2(probe_v(t, 2 * lane), probe_v(t, 2 * lane + 1));
+        float m[PROBE_ROWS], l[PROBE_ROWS], acc[PROBE_ROWS][2];
+#pragma unroll
+        for (int r = 0; r < PROBE_ROWS; ++r) {
+            m[r] = neg_inf();
+            l[r] = 0.f;
+            acc[r][0] = acc[r][1] = 0.f;
+        }
+        for (int it = 0; it < items; ++it) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) opaque(kk[j]);
+#pragma unroll
+            for (int t = 0; t < PAGE; ++t) opaque(vv[t]);
+#pragma unroll
+            for (int r = 0; r < PROBE_ROWS; ++r) {
+                // S[r][token c]: the lane's 32 channels, then the 4 lane groups
+                float sr = 0.f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    sr = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, kk[j]),
+                                                __builtin_bit_cast(h2, qq[r][j]), sr, false);
+                sr += __shfl_xor(sr, 16);
+                sr += __shfl_xor(sr, 32);
+                const float x = sr * scale_log2;
+                const float m_new = fmaxf(m[r], row16_max(x));
+                const float alpha = fast_exp2(m[r] - m_new);
+                const float p = fast_exp2(x - m_new);
+                l[r] = l[r] * alpha + row16_sum(p);
+                m[r] = m_new;
+                acc[r][0] *= alpha;
+                acc[r][1] *= alpha;
+                // O[r][2 lane + e] += P[r][t] V[t][2 lane + e], P broadcast
+#pragma unroll
+                for (int t = 0; t < PAGE; ++t) {
+                    const float pt = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), t));
+                    const h2 v2 = __builtin_bit_cast(h2, vv[t]);
+                    acc[r][0] = fmaf(pt, (float)v2.x, acc[r][0]);
+                    acc[r][1] = fmaf(pt, (float)v2.y, acc[r][1]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < PROBE_ROWS; ++r) {
+            o[r * HEAD_DIM + 2 * lane] = acc[r][0] / l[r];
+            o[r * HEAD_DIM + 2 * lane + 1] = acc[r][1] / l[r];
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_compute_probe(int mode, int groups, int items, float scale, float* out,
+                                hipStream_t stream) {
+    const float scale_log2 = scale * LOG2E;
+    if (mode == 0)
+        hipLaunchKernelGGL(compute_probe_kernel<0>, dim3(groups), dim3(WAVE * PROBE_WAVES), 0, stream,
+                           items, scale_log2, out);
+    else
+        hipLaunchKernelGGL(compute_probe_kernel<1>, dim3(groups), dim3(WAVE * PROBE_WAVES), 0, stream,
+                           items, scale_log2, out);
+    return hipGetLastError();
+}
+
 }  // namespace ls
