@@ -118,6 +118,26 @@ int ls_paged_sparse_fp16(const void* q, const int64_t* q_strides, const void* k_
                          int head_dim, int page, int num_splits, int max_seq_len, float softmax_scale,
                          void* stream);
 
+/* Sparse attention in one launch: each workgroup selects its sequence's
+ * page lists from scores [B, H_kv, score_pages] fp32 (score_strides[2] =
+ * (b, h); ls_page_scores writes them) as ls_page_select does (sorted = 0:
+ * the sequence's budget max(recent+1, ceilf(ratio*pages)), capped at its
+ * pages and k, of its best pages in page order, ties to the lower page),
+ * then attends them as ls_paged_sparse_fp16 attends such a list; the same
+ * list and partition, without the list ever leaving the chip.  k <=
+ * score_pages <= 8192; ceil(k / num_splits) <= 1024.  Replaces
+ * sparse_attention's select + sparse_decode (kernels/cuda/paged_sparse.py:
+ * 222-251, select :164-168). */
+int ls_sparse_attention_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
+                             const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                             const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                             const int32_t* seq_lens, const float* scores,
+                             const int64_t* score_strides, int score_pages, int k, float ratio,
+                             int recent, void* out, const int64_t* out_strides, float* workspace,
+                             int32_t* counters, int batch, int kv_heads, int n_rep,
+                             int head_dim, int page, int num_splits, int max_seq_len,
+                             float softmax_scale, void* stream);
+
 /* Merge split partials: combine_splits / _combine_kernel
  * (kernels/gqa/paged_decode.py:689-706, :422-471).  acc [B, H, S, rows, 128]
  * with strides acc_strides[4] = (b, h, s, row); m and l [B, H, S, rows] with

@@ -134,7 +134,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 9; }
+int ls_abi_version(void) { return 10; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -249,6 +249,46 @@ int ls_paged_sparse_fp16(const void* q, const int64_t* q_strides, const void* k_
     a.ratio = ratio;
     a.recent = recent;
     return hip_status(ls::launch_decode(a, (hipStream_t)stream), "ls_paged_sparse_fp16");
+}
+
+int ls_sparse_attention_fp16(const void* q, const int64_t* q_strides, const void* k_pool,
+                             const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                             const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                             const int32_t* seq_lens, const float* scores,
+                             const int64_t* score_strides, int score_pages, int k, float ratio,
+                             int recent, void* out, const int64_t* out_strides, float* workspace,
+                             int32_t* counters, int batch, int kv_heads, int n_rep,
+                             int head_dim, int page, int num_splits, int max_seq_len,
+                             float softmax_scale, void* stream) {
+    int rc = check_common(q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables,
+                          max_pages, seq_lens, out, out_strides, workspace,
+                          counters, batch, kv_heads, n_rep, head_dim, page, num_splits, 2);
+    if (rc) return rc;
+    if (!scores || !score_strides) return fail(LS_ERR_INVALID, "needs page scores");
+    if (score_pages < 1 || score_pages > ls::SELECT_MAX_PAGES)
+        return fail(LS_ERR_INVALID, "score_pages must be in [1, %d], got %d",
+                    ls::SELECT_MAX_PAGES, score_pages);
+    if (k < 0 || k > score_pages)
+        return fail(LS_ERR_INVALID, "k must be in [0, score_pages], got %d", k);
+    // every split's share of a list must fit the group's item table
+    if ((k + num_splits - 1) / num_splits > ls::SELECT_SPLIT_ENTRIES)
+        return fail(LS_ERR_INVALID,
+                    "k / num_splits must be at most %d (k %d, num_splits %d): use more splits",
+                    ls::SELECT_SPLIT_ENTRIES, k, num_splits);
+    if (batch == 0) return LS_OK;
+    ls::DecodeParams a;
+    fill_common(a, q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables, bt_stride,
+                max_pages, seq_lens, out, out_strides, workspace, counters, batch,
+                kv_heads, n_rep, num_splits, max_seq_len, softmax_scale);
+    a.kind = ls::KV_FP16;
+    a.scores = scores;
+    a.ssc_b = score_strides[0];
+    a.ssc_h = score_strides[1];
+    a.score_pages = score_pages;
+    a.num_sel = k;
+    a.ratio = ratio;
+    a.recent = recent;
+    return hip_status(ls::launch_decode(a, (hipStream_t)stream), "ls_sparse_attention_fp16");
 }
 
 int ls_combine_splits(const float* part_acc, const int64_t* acc_strides, const float* part_m,

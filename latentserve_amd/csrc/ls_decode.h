@@ -8,6 +8,10 @@ namespace ls {
 
 enum KvKind { KV_FP16 = 0, KV_INT8 = 1 };
 
+// List entries one group of a selecting page-subset walk keeps in its item
+// table (a split's share of the list must fit).
+constexpr int SELECT_SPLIT_ENTRIES = 1024;
+
 // Everything one decode launch reads.  Strides are in elements.
 struct DecodeParams {
     const _Float16* q;
@@ -36,6 +40,9 @@ struct DecodeParams {
     int num_sel;
     float ratio;
     int recent;
+    const float* scores;               // non-null: page-subset walk whose list the kernel
+    int64_t ssc_b, ssc_h;              // selects itself from page scores [B, H, score_pages]
+    int score_pages;                   // (num_sel = the list width k)
     float* work;                       // [B * S, H] records of NR*128 + 32 floats:
                                        // acc[NR][128], m[16] (natural log), l[16]
     int pages_per_split;               // > 0: dense walk partition given by the host

@@ -47,6 +47,7 @@
 
 #include "ls_common.h"
 #include "ls_decode.h"
+#include "ls_select.h"
 
 namespace ls {
 
@@ -534,7 +535,9 @@ __device__ __forceinline__ int claim_item(int* counter, int lane) {
 }
 __device__ __forceinline__ int claimed_item(int raw) { return __builtin_amdgcn_readlane(raw, 0); }
 
-template <int KIND, bool ASYM, bool HAS_RES, bool SPARSE, int NWT, int HG, int ABL = 0>
+// SPARSE: 0 the dense walk; 1 a page-subset walk over the caller's lists;
+// 2 a page-subset walk whose lists the group selects from page scores.
+template <int KIND, bool ASYM, bool HAS_RES, int SPARSE, int NWT, int HG, int ABL = 0>
 __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodeParams a) {
     // Pages in flight ahead of the one being computed.  INT8 keeps one: a
     // second buffer would take its kernels past 256 registers, to one wave
@@ -722,7 +725,43 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     };
     auto fill_table = [&]() {
         if (!cached) return;
-        if (SPARSE) {
+        if constexpr (SPARSE == 2) {
+            // Each 256-thread half selects its head's list from the page
+            // scores (the selection kernel's radix select; in LDS the merge
+            // buffer holds only after the walk) and keeps the entries of
+            // this split's range, resolved to blocks.  (A threshold
+            // bisection without LDS atomics measured slower: 63 against
+            // 52 us for c5.)
+            static_assert(WAVE * NWT == 256 * HG, "one 256-thread group a head");
+            static_assert(CAP >= SELECT_SPLIT_ENTRIES, "a split's entries fit the table");
+            const int hh = threadIdx.x / 256, tid = threadIdx.x % 256;
+            SelectSmem* ssm = reinterpret_cast<SelectSmem*>(&sm.acc[0][0][0][0]);
+            const float* row = a.scores + (int64_t)b * a.ssc_b + (int64_t)(h0 + hh) * a.ssc_h;
+            // the selection reports pages only; their blocks are looked up
+            // below, one independent load a thread (a load per reported page
+            // would chain a thread's round trips)
+            auto emit = [&](int pos, int pg) {
+                if (pos >= lo && pos < hi) sm.ent[(hh * 2 + 1) * CAP + pos - lo] = pg;
+            };
+            if (a.score_pages <= 8 * 256)
+                select_row_k<false, 8>(row, a.score_pages, n_list, 0, tid, nullptr, ssm[hh],
+                                       nullptr, emit);
+            else
+                select_row_k<false, 32>(row, a.score_pages, n_list, 0, tid, nullptr, ssm[hh],
+                                        nullptr, emit);
+            __syncthreads();
+            const int32_t* trow = a.block_tables + (int64_t)b * a.sbt_b;
+            for (int i = threadIdx.x; i < n_ent * HG; i += WAVE * NWT) {
+                const int hs = i / n_ent, e = i % n_ent;
+                const int pg = sm.ent[(hs * 2 + 1) * CAP + e];
+                int blk = -1;
+                if (pg >= 0 && pg < num_pages) {
+                    blk = trow[pg];
+                    if (blk < 0 || blk >= a.num_blocks) blk = -1;
+                }
+                sm.ent[(hs * 2) * CAP + e] = blk;
+            }
+        } else if (SPARSE) {
             for (int i = threadIdx.x; i < n_ent * HG; i += WAVE * NWT) {
                 const int hh = i / n_ent, e = i % n_ent;
                 int blk, pg;
@@ -816,13 +855,19 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         auto issue = [&](int slot, int it) { issue_with(resolve, slot, it); };
         // The first items are fixed (wave wv takes wv, wv + NWT, ...): their
         // loads are in flight while the group fills the item table and meets
-        // at the barrier.
+        // at the barrier (a selecting group knows its items only after).
+        if (SPARSE == 2) {
+            fill_table();
+            __syncthreads();
+        }
 #pragma unroll
         for (int u = 0; u < PF_DEPTH; ++u)
             issue_with([&](int i, int& blk, int& pg, int& hh) { first(u, i, blk, pg, hh); }, u,
                        wv + u * NWT);
-        fill_table();
-        __syncthreads();
+        if (SPARSE != 2) {
+            fill_table();
+            __syncthreads();
+        }
         int it_n = wv + PF_DEPTH * NWT;
         if (item[0] >= n_items) return;
         while (true) {
@@ -861,7 +906,10 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // fallback load shares the fast path's control flow.
     auto first_fixed = [&](int u, int i, int& blk, int& pg, int& hh) { resolve_first(u, i, blk, pg, hh); };
     auto first_mem = [&](int, int i, int& blk, int& pg, int& hh) { resolve_mem(i, blk, pg, hh); };
-    if (cached && spec_ok)
+    auto first_lds = [&](int, int i, int& blk, int& pg, int& hh) { resolve_lds(i, blk, pg, hh); };
+    if (SPARSE == 2)
+        walk(resolve_lds, first_lds);      // the host keeps every range within the table
+    else if (cached && spec_ok)
         walk(resolve_lds, first_fixed);
     else if (cached)
         walk(resolve_lds, first_mem);
@@ -1021,7 +1069,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
 
 constexpr int NWAVES = 4;
 
-template <int KIND, bool ASYM, bool HAS_RES, bool SPARSE, int ABL = 0>
+template <int KIND, bool ASYM, bool HAS_RES, int SPARSE, int ABL = 0>
 static hipError_t launch_t(const DecodeParams& a, hipStream_t stream) {
     // Heads in pairs when the head count allows: both halves of every token
     // row are then read together (the fp16 walk; INT8 keeps one head per
@@ -1060,25 +1108,26 @@ static int ablation() {
 }
 
 static hipError_t launch_kernel(const DecodeParams& a, hipStream_t stream) {
-    if (a.sel) return launch_t<KV_FP16, false, false, true>(a, stream);
+    if (a.scores) return launch_t<KV_FP16, false, false, 2>(a, stream);
+    if (a.sel) return launch_t<KV_FP16, false, false, 1>(a, stream);
     if (a.kind == KV_FP16 && ablation() != 0) {
         const int abl = ablation();
-        if (abl == 1) return launch_t<KV_FP16, false, false, false, 1>(a, stream);
-        if (abl == 2) return launch_t<KV_FP16, false, false, false, 2>(a, stream);
-        return launch_t<KV_FP16, false, false, false, 3>(a, stream);
+        if (abl == 1) return launch_t<KV_FP16, false, false, 0, 1>(a, stream);
+        if (abl == 2) return launch_t<KV_FP16, false, false, 0, 2>(a, stream);
+        return launch_t<KV_FP16, false, false, 0, 3>(a, stream);
     }
-    if (a.kind == KV_FP16) return launch_t<KV_FP16, false, false, false>(a, stream);
+    if (a.kind == KV_FP16) return launch_t<KV_FP16, false, false, 0>(a, stream);
     const bool asym = a.k_zero != nullptr, res = a.k_res != nullptr;
     if (ablation() != 0 && !asym && !res) {
         const int abl = ablation();
-        if (abl == 1) return launch_t<KV_INT8, false, false, false, 1>(a, stream);
-        if (abl == 2) return launch_t<KV_INT8, false, false, false, 2>(a, stream);
-        return launch_t<KV_INT8, false, false, false, 3>(a, stream);
+        if (abl == 1) return launch_t<KV_INT8, false, false, 0, 1>(a, stream);
+        if (abl == 2) return launch_t<KV_INT8, false, false, 0, 2>(a, stream);
+        return launch_t<KV_INT8, false, false, 0, 3>(a, stream);
     }
-    if (asym && res) return launch_t<KV_INT8, true, true, false>(a, stream);
-    if (asym) return launch_t<KV_INT8, true, false, false>(a, stream);
-    if (res) return launch_t<KV_INT8, false, true, false>(a, stream);
-    return launch_t<KV_INT8, false, false, false>(a, stream);
+    if (asym && res) return launch_t<KV_INT8, true, true, 0>(a, stream);
+    if (asym) return launch_t<KV_INT8, true, false, 0>(a, stream);
+    if (res) return launch_t<KV_INT8, false, true, 0>(a, stream);
+    return launch_t<KV_INT8, false, false, 0>(a, stream);
 }
 
 hipError_t launch_decode(const DecodeParams& a, hipStream_t stream) {

@@ -27,6 +27,7 @@
 //    take several microseconds to return under that traffic.
 #include "ls_common.h"
 #include "ls_sparse.h"
+#include "ls_select.h"
 
 namespace ls {
 
@@ -62,228 +63,6 @@ __device__ __forceinline__ void h8_to_f8(u4 x, float* f) {
     }
 }
 
-// Order-preserving map float -> uint32 (larger float, larger key); -0 and
-// +0 compare equal, as they do for the reference's torch.topk.
-__device__ __forceinline__ uint32_t order_key(float f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    u = u == 0x80000000u ? 0u : u;
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Pages a sequence of length L attends with this ratio: the rule of the
-// sparse decode kernel (paged_sparse_fp16.cu:242-247), capped at k.
-__device__ __forceinline__ int budget_pages(int L, int P, float ratio, int recent, int k) {
-    int pages = L > 0 ? (L + PAGE - 1) / PAGE : 0;
-    pages = pages < P ? pages : P;
-    if (!(ratio > 0.f)) return k;
-    int want;
-    if (ratio >= 1.f) {
-        want = pages;
-    } else {
-        want = (int)ceilf(ratio * (float)pages);
-        want = want > recent + 1 ? want : recent + 1;
-    }
-    want = want < pages ? want : pages;
-    return want < k ? want : k;
-}
-
-constexpr int SEL_THREADS = 256;
-constexpr int SEL_KPT = SELECT_MAX_PAGES / SEL_THREADS;   // keys per thread
-
-struct SelectSmem {
-    uint32_t hist[2][256];
-    uint32_t wsum[4];
-    int found[4];
-};
-
-// Inclusive prefix sum over the 256 threads of a group.
-__device__ __forceinline__ uint32_t group_scan(uint32_t v, uint32_t* wsum) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = (uint32_t)__builtin_amdgcn_ds_bpermute((lane - o) << 2, (int)v);
-        if (lane >= o) v += t;
-    }
-    if (lane == 63) wsum[wv] = v;
-    __syncthreads();
-    for (int w = 0; w < wv; ++w) v += wsum[w];
-    __syncthreads();
-    return v;
-}
-
-// Select from one row of P scores: out[0, n1) = the n1 best pages, out[n1,
-// n2) = the next n2 - n1 (n1 <= n2 <= P), each part in page order.  Order
-// among equal scores: lower page first.  With SORTED (n1 == n2) the n2 pages
-// are written best first instead.
-//
-// KPT keys per thread (P <= 256 * KPT): the loops over a thread's keys are
-// fully unrolled at exactly KPT, so their cost follows the row length.
-template <bool SORTED, int KPT>
-__device__ __attribute__((always_inline)) void select_row_k(const float* srow, int P, int n1,
-                                                            int n2, int32_t* out, SelectSmem& sm,
-                                                            uint32_t* skeys) {
-    const int tid = threadIdx.x;
-    const int i0 = tid * KPT;
-    int cnt = P - i0;
-    cnt = cnt < 0 ? 0 : (cnt > KPT ? KPT : cnt);
-    uint32_t key[KPT];
-    {
-        // unconditional loads (clamped index) so they all issue back to back
-        float f[KPT];
-        const int last = P > 0 ? P - 1 : 0;
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) f[j] = P > 0 ? srow[i0 + j < last ? i0 + j : last] : 0.f;
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) key[j] = j < cnt ? order_key(f[j]) : 0u;
-    }
-
-    // ---- radix select of the n1-th and n2-th largest keys ----
-    uint32_t pre0 = 0, pre1 = 0, msk = 0;
-    int rem0 = n1, rem1 = n2;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        sm.hist[0][tid] = 0;
-        sm.hist[1][tid] = 0;
-        __syncthreads();
-        // A thread's keys are adjacent pages whose leading digits mostly
-        // agree (one exponent for the whole row): count runs of equal digits
-        // and add each run once, instead of one LDS atomic per key on a
-        // handful of hot bins.
-        uint32_t d0 = 256u, n0 = 0u, d1 = 256u, n1c = 0u;
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) {
-            if (j < cnt) {
-                const uint32_t d = (key[j] >> shift) & 255u;
-                if ((key[j] & msk) == pre0) {
-                    if (d != d0) {
-                        if (n0) atomicAdd(&sm.hist[0][d0], n0);
-                        d0 = d;
-                        n0 = 0u;
-                    }
-                    ++n0;
-                }
-                if ((key[j] & msk) == pre1) {
-                    if (d != d1) {
-                        if (n1c) atomicAdd(&sm.hist[1][d1], n1c);
-                        d1 = d;
-                        n1c = 0u;
-                    }
-                    ++n1c;
-                }
-            }
-        }
-        if (n0) atomicAdd(&sm.hist[0][d0], n0);
-        if (n1c) atomicAdd(&sm.hist[1][d1], n1c);
-        __syncthreads();
-        const int bin = 255 - tid;   // thread order = descending digit
-        const uint32_t c = sm.hist[0][bin] | (sm.hist[1][bin] << 16);
-        const uint32_t incl = group_scan(c, sm.wsum);
-        const uint32_t excl = incl - c;
-        const int ci0 = (int)(incl & 0xFFFFu), ce0 = (int)(excl & 0xFFFFu);
-        const int ci1 = (int)(incl >> 16), ce1 = (int)(excl >> 16);
-        if (ce0 < rem0 && ci0 >= rem0) {
-            sm.found[0] = bin;
-            sm.found[1] = rem0 - ce0;
-        }
-        if (ce1 < rem1 && ci1 >= rem1) {
-            sm.found[2] = bin;
-            sm.found[3] = rem1 - ce1;
-        }
-        __syncthreads();
-        if (rem0 > 0) {
-            pre0 |= (uint32_t)sm.found[0] << shift;
-            rem0 = sm.found[1];
-        }
-        if (rem1 > 0) {
-            pre1 |= (uint32_t)sm.found[2] << shift;
-            rem1 = sm.found[3];
-        }
-        msk |= 255u << shift;
-        __syncthreads();
-    }
-    // threshold keys pre0 / pre1; rem0 / rem1 = how many keys equal to them
-    // belong to the set (the lowest pages first)
-    const bool want0 = n1 > 0, want1 = n2 > 0;
-
-    uint32_t e = 0;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j)
-        if (j < cnt) e += (key[j] == pre0 ? 1u : 0u) + (key[j] == pre1 ? 0x10000u : 0u);
-    uint32_t incl = group_scan(e, sm.wsum);
-    uint32_t excl = incl - e;
-    int r0 = (int)(excl & 0xFFFFu), r1 = (int)(excl >> 16);
-    uint32_t ma = 0, mb = 0;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-        if (j < cnt) {
-            bool a0, a1;
-            if (key[j] == pre0) {
-                a0 = want0 && r0 < rem0;
-                ++r0;
-            } else {
-                a0 = want0 && key[j] > pre0;
-            }
-            if (key[j] == pre1) {
-                a1 = want1 && r1 < rem1;
-                ++r1;
-            } else {
-                a1 = want1 && key[j] > pre1;
-            }
-            ma |= (a0 ? 1u : 0u) << j;
-            mb |= (a1 && !a0 ? 1u : 0u) << j;
-        }
-    }
-    const uint32_t ab = (uint32_t)__builtin_popcount(ma) | ((uint32_t)__builtin_popcount(mb) << 16);
-    incl = group_scan(ab, sm.wsum);
-    excl = incl - ab;
-    int pa = (int)(excl & 0xFFFFu), pb = n1 + (int)(excl >> 16);
-    if constexpr (!SORTED) {
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) {
-            if ((ma >> j) & 1u) out[pa++] = i0 + j;
-            if ((mb >> j) & 1u) out[pb++] = i0 + j;
-        }
-    } else {
-        // the set, in page order, into LDS; then rank each member against it
-        int pos[KPT];
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) {
-            pos[j] = pa;
-            if ((ma >> j) & 1u) skeys[pa++] = key[j];
-        }
-        __syncthreads();
-        int rank[KPT];
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) rank[j] = 0;
-        for (int m = 0; m < n1; ++m) {
-            const uint32_t km = skeys[m];
-#pragma unroll
-            for (int j = 0; j < KPT; ++j)
-                rank[j] += (km > key[j] || (km == key[j] && m < pos[j])) ? 1 : 0;
-        }
-#pragma unroll
-        for (int j = 0; j < KPT; ++j)
-            if ((ma >> j) & 1u) out[rank[j]] = i0 + j;
-    }
-}
-
-template <bool SORTED>
-__device__ __attribute__((always_inline)) void select_row(const float* srow, int P, int n1, int n2,
-                                                          int32_t* out, SelectSmem& sm,
-                                                          uint32_t* skeys) {
-    const int kpt = (P + SEL_THREADS - 1) / SEL_THREADS;
-    if (kpt <= 1)
-        select_row_k<SORTED, 1>(srow, P, n1, n2, out, sm, skeys);
-    else if (kpt <= 2)
-        select_row_k<SORTED, 2>(srow, P, n1, n2, out, sm, skeys);
-    else if (kpt <= 4)
-        select_row_k<SORTED, 4>(srow, P, n1, n2, out, sm, skeys);
-    else if (kpt <= 8)
-        select_row_k<SORTED, 8>(srow, P, n1, n2, out, sm, skeys);
-    else if (kpt <= 16)
-        select_row_k<SORTED, 16>(srow, P, n1, n2, out, sm, skeys);
-    else
-        select_row_k<SORTED, 32>(srow, P, n1, n2, out, sm, skeys);
-}
 
 // NR: query rows per KV head (a compile-time count keeps only those rows'
 // registers, which sets how many index groups a CU holds at once).
@@ -363,8 +142,9 @@ __global__ __launch_bounds__(256) void page_select_kernel(SelectParams a) {
     const int h = blockIdx.x, b = blockIdx.y;
     const int L = a.seq_lens ? a.seq_lens[b] : 0;
     const int n1 = SORTED ? a.k : budget_pages(L, a.P, a.ratio, a.recent, a.k);
+    int32_t* out = a.sel + (int64_t)b * a.sl_b + (int64_t)h * a.sl_h;
     select_row<SORTED>(a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h, a.P, n1, a.k,
-                       a.sel + (int64_t)b * a.sl_b + (int64_t)h * a.sl_h, sm, skeys);
+                       (int)threadIdx.x, out, sm, skeys, [&](int pos, int pg) { out[pos] = pg; });
 }
 
 // grid (B, H), 64 threads: two channels per lane.

@@ -5,9 +5,12 @@ Mirrors the reference's kernels/cuda/paged_sparse.py: ``budget`` (:74-78),
 (:104-123), ``select`` (:164-168), ``budgets`` (:171-182), ``sparse_decode``
 (:185-219) and ``sparse_attention`` (:222-251), all on HIP kernels.
 
-Per layer per decode step the pipeline is two launches: index + select
-(one fused kernel: the last index group of each (sequence, head) selects)
-and the page-subset decode. Nothing syncs with the host, so the step is
+Per layer per decode step ``sparse_attention`` is two launches: the page
+index (scores) and a page-subset decode whose workgroups select their own
+lists from the scores (ls_sparse_attention_fp16: the selection kernel's
+radix select in each group's prologue, the same lists and partition as
+select + sparse_decode).  ``fused=False`` runs the three launches (index,
+select, decode) instead.  Nothing syncs with the host, so the step is
 capturable in a HIP graph.
 """
 
@@ -216,15 +219,19 @@ def sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel,
     return buf[:, :, :n_rep] if out is None else out
 
 
+SELECT_SPLIT_ENTRIES = 1024    # list entries a selecting group keeps (a split's share)
+
+
 def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
                      ratio: float = 0.25, recent: int = 2,
                      num_splits: Optional[int] = None, max_seq_len: Optional[int] = None,
                      softmax_scale: Optional[float] = None,
                      scoring: str = "bounds",
-                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Index, select, attend (two launches). The list width k follows
-    `max_seq_len` (the context) when given, else the table's width; each
-    sequence then attends its own budget for its current length."""
+                     out: Optional[torch.Tensor] = None, fused: bool = True) -> torch.Tensor:
+    """Index, select, attend. The list width k follows `max_seq_len` (the
+    context) when given, else the table's width; each sequence then attends
+    its own budget for its current length.  Two launches (the decode
+    selects), or three with ``fused=False``."""
     if scoring != "bounds":
         raise ValueError(f"scoring {scoring!r} is not provided by the HIP backend "
                          "(only 'bounds')")
@@ -232,6 +239,33 @@ def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
     pages = block_tables.shape[1] if max_seq_len is None else min(
         block_tables.shape[1], -(-int(max_seq_len) // page))
     k = budget(ratio, pages, recent)
-    sel = index_select(q, kmin, kmax, block_tables, seq_lens, k, ratio, recent)
-    return sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel, num_splits,
-                         softmax_scale, ratio=ratio, recent=recent, out=out)
+    if not fused:
+        sel = index_select(q, kmin, kmax, block_tables, seq_lens, k, ratio, recent)
+        return sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel, num_splits,
+                             softmax_scale, ratio=ratio, recent=recent, out=out)
+    reason = pdh.ineligible_reason(q, k_pool)
+    if reason is None and k_pool.dtype != torch.float16:
+        reason = "the page-subset kernel reads fp16 pools"
+    if reason is not None:
+        raise ValueError(f"sparse_attention: {reason}")
+    pdh._check_common(q, k_pool, v_pool, block_tables, seq_lens)
+    if block_tables.shape[1] > SELECT_MAX_PAGES:
+        raise ValueError(f"selection supports up to {SELECT_MAX_PAGES} pages, "
+                         f"got {block_tables.shape[1]}")
+    scores = page_scores(q, kmin, kmax, block_tables, seq_lens, recent)
+    b, h, n_rep, d = q.shape
+    splits = num_splits or pdh.choose_splits(b, h, k, q.device)
+    splits = max(1, min(splits, max(1, k), pdh.MAX_SPLITS))
+    splits = max(splits, -(-k // SELECT_SPLIT_ENTRIES))
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
+    buf, work, cnt = pdh._buffers("sparse", b, h, splits, n_rep, q.device)
+    target = buf if out is None else pdh.check_out(out, q)
+    P, S = _lib.ptr, _lib.strides
+    rc = _lib.lib().ls_sparse_attention_fp16(
+        P(q), S(q, 3), P(k_pool), P(v_pool), S(k_pool, 3), k_pool.shape[0],
+        P(block_tables), block_tables.stride(0), block_tables.shape[1], P(seq_lens),
+        P(scores), S(scores, 2), scores.shape[2], k, float(ratio), int(recent),
+        P(target), S(target, 3), P(work), P(cnt), b, h, n_rep, d, page,
+        splits, 0, float(scale), _lib.stream_of(q.device))
+    _lib.check(rc, "ls_sparse_attention_fp16")
+    return buf[:, :, :n_rep] if out is None else out

@@ -198,6 +198,29 @@ def test_sparse_attention_end_to_end(ratio):
         assert_close(out, oracle.paged_decode(q, k, v, t, l), ATOL, RTOL, "full = dense")
 
 
+@pytest.mark.parametrize("width,lens,ratio,splits", [
+    (256, [256 * 16, 2500, 700, 40], 0.5, 1),          # one split: the whole list a group
+    (256, [256 * 16, 3333, 17], 0.3, 7),
+    (3000, [3000 * 16, 10000, 1], 0.5, None),          # rows past 2048 pages: 32 keys a thread
+    (2200, [2200 * 16], 1.0, 1),                       # k 2200 > 1024 a split: splits raised to 3
+])
+def test_selecting_decode_attends_the_selected_pages(width, lens, ratio, splits):
+    """The decode that selects its own lists from the scores attends what
+    index_select's lists give the oracle, and agrees with the three-launch
+    path."""
+    q, k, v, t, l, kmin, kmax = index_case(lens, width=width, seed=width + len(lens))
+    Q, K, V, T, L, KN, KX = dev(q, k, v, t, l, kmin, kmax)
+    out = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=ratio, num_splits=splits)
+    three = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=ratio, num_splits=splits,
+                                  fused=False)
+    torch.cuda.synchronize()
+    kk = ps().budget(ratio, width)
+    sel = ps().index_select(Q, KN, KX, T, L, kk, ratio).cpu().numpy()
+    want = oracle.sparse_decode(q, k, v, t, l, sel, ratio=ratio, recent=2)
+    assert_close(out.float().cpu().numpy(), want, ATOL, RTOL, f"w={width} r={ratio} s={splits}")
+    assert (out.float() - three.float()).abs().max().item() < 1e-3
+
+
 def test_sparse_attention_graph_replays():
     width = 128
     q, k, v, t, l, kmin, kmax = index_case([width * 16, 900], width=width, seed=4)
