@@ -730,8 +730,10 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             // scores (the selection kernel's radix select; in LDS the merge
             // buffer holds only after the walk) and keeps the entries of
             // this split's range, resolved to blocks.  (A threshold
-            // bisection without LDS atomics measured slower: 63 against
-            // 52 us for c5.)
+            // bisection without LDS atomics measured slower, 25 against 10
+            // us for the selection alone: at one wave a SIMD the select is
+            // bound by its dependent instruction latency, and the bisection
+            // has the longer chain.)
             static_assert(WAVE * NWT == 256 * HG, "one 256-thread group a head");
             static_assert(CAP >= SELECT_SPLIT_ENTRIES, "a split's entries fit the table");
             const int hh = threadIdx.x / 256, tid = threadIdx.x % 256;

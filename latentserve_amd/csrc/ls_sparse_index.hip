@@ -143,8 +143,9 @@ __global__ __launch_bounds__(256) void page_select_kernel(SelectParams a) {
     const int L = a.seq_lens ? a.seq_lens[b] : 0;
     const int n1 = SORTED ? a.k : budget_pages(L, a.P, a.ratio, a.recent, a.k);
     int32_t* out = a.sel + (int64_t)b * a.sl_b + (int64_t)h * a.sl_h;
-    select_row<SORTED>(a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h, a.P, n1, a.k,
-                       (int)threadIdx.x, out, sm, skeys, [&](int pos, int pg) { out[pos] = pg; });
+    const float* srow = a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h;
+    auto emit = [&](int pos, int pg) { out[pos] = pg; };
+    select_row<SORTED>(srow, a.P, n1, a.k, (int)threadIdx.x, out, sm, skeys, emit);
 }
 
 // grid (B, H), 64 threads: two channels per lane.
