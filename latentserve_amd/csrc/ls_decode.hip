@@ -635,7 +635,8 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             const int safe_blk = (unsigned)blk < (unsigned)a.num_blocks ? blk : 0;
             load_page<KIND, ASYM, HAS_RES>(a, buf[slot], safe_blk, -1, 0, 0, h0 + hh, g, c);
         } else {
-            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], ok ? blk : 0, ok ? pg : -1, npages, rrow,
+            // (the walk never holds the residual page: it is computed apart)
+            load_page<KIND, ASYM, false>(a, buf[slot], ok ? blk : 0, ok ? pg : -1, npages, rrow,
                                            h0 + hh, g, c);
         }
     };
@@ -704,7 +705,12 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         hi = (int)((long long)(gw.s + 1) * n_list / Sb);
     }
     const int n_ent = hi > lo ? hi - lo : 0;
-    const int n_items = n_ent * HG;
+    // INT8 with a residual: the sequence's last page (K from the fp16
+    // residual) is not a walk item; one wave of the group whose range ends
+    // the sequence computes it apart, so the walk's page buffers and compute
+    // carry INT8 pages only (their residual branch cost 3 us at c4).
+    const bool ends_seq = HAS_RES && n_ent > 0 && hi == num_pages;
+    const int n_items = (n_ent - (ends_seq ? 1 : 0)) * HG;
 
     // Resolve the group's entries to (block, page) once, into LDS (the merge
     // buffer, idle until the walk ends).  Block ids outside the pool, list
@@ -845,6 +851,18 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                !(HAS_RES && pg == num_pages - 1 && !res_ok);
     };
     auto walk = [&](auto resolve, auto first) {
+        if constexpr (HAS_RES) {
+            static_assert(HG == 1, "INT8 groups serve one head");
+            if (ends_seq && res_ok && wv == NWT - 1) {
+                const int lp = num_pages - 1;
+                const int blk = a.block_tables[(int64_t)b * a.sbt_b + lp];
+                const bool okb = blk >= 0 && blk < a.num_blocks;
+                PageBuf rb;
+                load_page<KIND, ASYM, true>(a, rb, okb ? blk : 0, lp, num_pages, res_row, h0, g, c);
+                compute_page<KIND, ASYM>(rb, st[0], qh[0], okb ? lp : -1, okb ? len : 0,
+                                         scale_log2, g, sm.kscale[wv]);
+            }
+        }
         auto issue_with = [&](auto res, int slot, int it) {
             int blk, pg, hh;
             res(it, blk, pg, hh);
