@@ -309,6 +309,28 @@ int ls_rope_write_decode(const void* qkv, int64_t qkv_stride, const int64_t* pos
                          const int64_t* bounds_strides, int batch, int hq, int hk, int head_dim,
                          void* stream);
 
+/* The fused q/k/v projection of one decode token per sequence with its
+ * finish in the epilogue: qkv = fp16(x[batch, K] . w^T + bias) for w
+ * [(hq + 2 hk) * head_dim, K] (never stored), then exactly what
+ * ls_rope_write_decode does with it (RoPE at positions[b], q folded to
+ * q_out, the rotated key and the value stored at slots[b], the page K
+ * bounds updated when kmin / kmax are given), bit-equal to ls_decode_gemm
+ * followed by ls_rope_write_decode.  Same arguments as those two (x and w
+ * as ls_decode_gemm: 16-byte aligned rows, K % 32 == 0, batch <= 64;
+ * head_dim % 16 == 0); refused (LS_ERR_INVALID) for sizes at which the
+ * GEMM would split K over workgroups.  Replaces the reference's qkv
+ * projection + rope_qk + paged cache write of the decode layer
+ * (model/attention/gqa.py:251-253, :283-344; cache/paged_cache.py). */
+int ls_decode_qkv_rope_write(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
+                             int w_packed, const void* bias, int K, const int64_t* positions,
+                             const void* cos,
+                             const void* sin, int64_t table_stride, int table_rows,
+                             const int64_t* slots, void* k_pool, void* v_pool,
+                             const int64_t* kv_strides, int num_blocks, int page, void* q_out,
+                             const int64_t* q_strides, void* kmin, void* kmax,
+                             const int64_t* bounds_strides, int batch, int hq, int hk,
+                             int head_dim, void* stream);
+
 /* y[r] = ls_rms_norm of table row ids[r] (int64, clamped into [0,
  * table_rows)), and rows_out[r] = that table row (NULL to skip): the token
  * embedding lookup and the first layer's input norm in one launch
@@ -332,6 +354,20 @@ size_t ls_argmax_workspace_bytes(int rows, int n);
 int ls_argmax_rows(const void* x, int64_t x_stride, int64_t* out, int rows, int n,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Weights of the decode GEMMs packed for their launches: the 16-row tiles
+ * of the entry point's row order (kind 0: ls_decode_gemm, 1:
+ * ls_decode_gate_up_silu, w = [gate; up]; 2: ls_decode_qkv_rope_write,
+ * head_dim used), each 32-channel step of a tile 1 KiB in the order the
+ * lanes load it, tiles padded with zero rows.  Every weight load of a
+ * packed launch then reads 1 KiB contiguous (a row-major weight gives 64
+ * bytes of each of 16 rows).  `packed` holds ls_gemm_packed_bytes(N, K,
+ * kind, head_dim) bytes, 16-byte aligned; pass it as `w` with w_packed = 1
+ * (w_stride ignored) to the entry point of its kind.  No counterpart in
+ * the reference (its weights stay torch Linear tensors). */
+size_t ls_gemm_packed_bytes(int N, int K, int kind, int head_dim);
+int ls_pack_gemm_weight(const void* w, int64_t w_stride, int N, int K, int kind, int head_dim,
+                        void* packed, void* stream);
+
 /* y[M, N] = x[M, K] . w[N, K]^T (+ bias[N]) in fp16 with fp32 sums: the
  * projections of a decode step (torch Linear weight layout), M <= 64 rows.
  * Rows of x, w and y are strided (x_stride, w_stride, y_stride elements);
@@ -343,7 +379,7 @@ int ls_argmax_rows(const void* x, int64_t x_stride, int64_t* out, int rows, int 
  * reference's decoder layers (model/latentserve_qwen.py, model/fused.py),
  * which run as cuBLAS GEMMs. */
 int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
-                   const void* bias, void* y, int64_t y_stride, int M, int N, int K,
+                   int w_packed, const void* bias, void* y, int64_t y_stride, int M, int N, int K,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of device `workspace` ls_decode_gemm needs for these sizes: fp32
@@ -365,8 +401,8 @@ size_t ls_decode_gemm_workspace_bytes(int M, int N, int K);
  * reference's gate_up projection + silu_and_mul
  * (kernels/fused_elementwise.py:222-233, model/fused.py). */
 int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
-                           const void* bias, void* y, int64_t y_stride, int M, int inter, int K,
-                           void* stream);
+                           int w_packed, const void* bias, void* y, int64_t y_stride, int M,
+                           int inter, int K, void* stream);
 
 /* Measurement only, no counterpart in the reference: the decode kernel's
  * page compute alone, from registers (groups x 8 waves, each applying one

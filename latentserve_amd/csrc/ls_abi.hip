@@ -128,13 +128,69 @@ void fill_common(ls::DecodeParams& a, const void* q, const int64_t* q_strides, c
     a.scale = softmax_scale;
 }
 
+int make_rope_params(ls::RopeWriteParams& a, const void* qkv, int64_t qkv_stride,
+                     const int64_t* positions, const void* cos, const void* sin,
+                     int64_t table_stride, int table_rows, const int64_t* slots, void* k_pool,
+                     void* v_pool, const int64_t* kv_strides, int num_blocks, int page,
+                     void* q_out, const int64_t* q_strides, void* kmin, void* kmax,
+                     const int64_t* bounds_strides, int batch, int hq, int hk, int head_dim) {
+    if (!qkv || !positions || !cos || !sin || !slots || !k_pool || !v_pool || !kv_strides ||
+        !q_out || !q_strides)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim < 2 || head_dim > 1024 || head_dim % 2 != 0)
+        return fail(LS_ERR_INVALID, "head_dim must be even and in [2, 1024], got %d", head_dim);
+    if (hk < 1 || hq < 1 || hq % hk != 0 || hq + 2 * hk > 65535)
+        return fail(LS_ERR_INVALID, "hq must be a positive multiple of hk (hq %d, hk %d)", hq, hk);
+    if (batch < 0 || batch > 65535) return fail(LS_ERR_INVALID, "batch must be in [0, 65535]");
+    if (table_rows < 1 || num_blocks < 1 || page < 1)
+        return fail(LS_ERR_INVALID, "table_rows, num_blocks and page must be >= 1");
+    if ((kmin == nullptr) != (kmax == nullptr) || (kmin && !bounds_strides))
+        return fail(LS_ERR_INVALID, "kmin, kmax and bounds_strides must be given together");
+    a.qkv = qkv;
+    a.sqkv = qkv_stride;
+    a.pos = positions;
+    a.cos = cos;
+    a.sin = sin;
+    a.st = table_stride;
+    a.tab_rows = table_rows;
+    a.slots = slots;
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.sp_b = kv_strides[0];
+    a.sp_t = kv_strides[1];
+    a.sp_h = kv_strides[2];
+    a.num_blocks = num_blocks;
+    a.page = page;
+    a.q_out = q_out;
+    a.sq_b = q_strides[0];
+    a.sq_h = q_strides[1];
+    a.sq_r = q_strides[2];
+    a.kmin = kmin;
+    a.kmax = kmax;
+    a.sb_b = kmin ? bounds_strides[0] : 0;
+    a.sb_h = kmin ? bounds_strides[1] : 0;
+    a.B = batch;
+    a.hq = hq;
+    a.hk = hk;
+    a.d = head_dim;
+    return LS_OK;
+}
+
+// x rows 16-byte aligned holding K values; w the same, or packed (its
+// layout holds every row; only its base alignment matters).
+bool weight_ok(const void* x, int64_t x_stride, const void* w, int64_t w_stride, int w_packed,
+               int K) {
+    if (!aligned(x, 16) || x_stride % 8 != 0 || x_stride < K || !aligned(w, 16)) return false;
+    return w_packed || (w_stride % 8 == 0 && w_stride >= K);
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 10; }
+int ls_abi_version(void) { return 12; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -787,47 +843,61 @@ int ls_rope_write_decode(const void* qkv, int64_t qkv_stride, const int64_t* pos
                          const int64_t* q_strides, void* kmin, void* kmax,
                          const int64_t* bounds_strides, int batch, int hq, int hk, int head_dim,
                          void* stream) {
-    if (!qkv || !positions || !cos || !sin || !slots || !k_pool || !v_pool || !kv_strides ||
-        !q_out || !q_strides)
-        return fail(LS_ERR_INVALID, "null pointer argument");
-    if (head_dim < 2 || head_dim > 1024 || head_dim % 2 != 0)
-        return fail(LS_ERR_INVALID, "head_dim must be even and in [2, 1024], got %d", head_dim);
-    if (hk < 1 || hq < 1 || hq % hk != 0 || hq + 2 * hk > 65535)
-        return fail(LS_ERR_INVALID, "hq must be a positive multiple of hk (hq %d, hk %d)", hq, hk);
-    if (batch < 0 || batch > 65535) return fail(LS_ERR_INVALID, "batch must be in [0, 65535]");
-    if (table_rows < 1 || num_blocks < 1 || page < 1)
-        return fail(LS_ERR_INVALID, "table_rows, num_blocks and page must be >= 1");
-    if ((kmin == nullptr) != (kmax == nullptr) || (kmin && !bounds_strides))
-        return fail(LS_ERR_INVALID, "kmin, kmax and bounds_strides must be given together");
     ls::RopeWriteParams a;
-    a.qkv = qkv;
-    a.sqkv = qkv_stride;
-    a.pos = positions;
-    a.cos = cos;
-    a.sin = sin;
-    a.st = table_stride;
-    a.tab_rows = table_rows;
-    a.slots = slots;
-    a.k_pool = k_pool;
-    a.v_pool = v_pool;
-    a.sp_b = kv_strides[0];
-    a.sp_t = kv_strides[1];
-    a.sp_h = kv_strides[2];
-    a.num_blocks = num_blocks;
-    a.page = page;
-    a.q_out = q_out;
-    a.sq_b = q_strides[0];
-    a.sq_h = q_strides[1];
-    a.sq_r = q_strides[2];
-    a.kmin = kmin;
-    a.kmax = kmax;
-    a.sb_b = kmin ? bounds_strides[0] : 0;
-    a.sb_h = kmin ? bounds_strides[1] : 0;
-    a.B = batch;
-    a.hq = hq;
-    a.hk = hk;
-    a.d = head_dim;
+    const int rc = make_rope_params(a, qkv, qkv_stride, positions, cos, sin, table_stride,
+                                    table_rows, slots, k_pool, v_pool, kv_strides, num_blocks,
+                                    page, q_out, q_strides, kmin, kmax, bounds_strides, batch, hq,
+                                    hk, head_dim);
+    if (rc) return rc;
     return hip_status(ls::launch_rope_write_decode(a, (hipStream_t)stream), "ls_rope_write_decode");
+}
+
+int ls_decode_qkv_rope_write(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
+                             int w_packed, const void* bias, int K, const int64_t* positions,
+                             const void* cos,
+                             const void* sin, int64_t table_stride, int table_rows,
+                             const int64_t* slots, void* k_pool, void* v_pool,
+                             const int64_t* kv_strides, int num_blocks, int page, void* q_out,
+                             const int64_t* q_strides, void* kmin, void* kmax,
+                             const int64_t* bounds_strides, int batch, int hq, int hk,
+                             int head_dim, void* stream) {
+    ls::GemmParams a;
+    const int rc = make_rope_params(a.rope, x, 0, positions, cos, sin, table_stride, table_rows,
+                                    slots, k_pool, v_pool, kv_strides, num_blocks, page, q_out,
+                                    q_strides, kmin, kmax, bounds_strides, batch, hq, hk,
+                                    head_dim);
+    if (rc) return rc;
+    if (!w) return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim % 16 != 0) return fail(LS_ERR_INVALID, "head_dim must be a multiple of 16");
+    if (batch > ls::GEMM_MAX_M || K < 32 || K % 32 != 0)
+        return fail(LS_ERR_INVALID, "need batch <= %d and K a positive multiple of 32 (K %d)",
+                    ls::GEMM_MAX_M, K);
+    if (!weight_ok(x, x_stride, w, w_stride, w_packed, K))
+        return fail(LS_ERR_INVALID, "x and w rows must be 16-byte aligned and hold K values");
+    if (bias && !aligned(bias, 2)) return fail(LS_ERR_INVALID, "bias must be 2-byte aligned");
+    const int N = (hq + 2 * hk) * head_dim;
+    if (batch > 0 && ls::decode_gemm_splits(batch, N, K) != 1)
+        return fail(LS_ERR_INVALID,
+                    "K %d is too long to fuse at this width: use ls_decode_gemm, then "
+                    "ls_rope_write_decode", K);
+    if (batch == 0) return LS_OK;
+    a.x = x;
+    a.ldx = x_stride;
+    a.w = w;
+    a.ldw = w_stride;
+    a.w_packed = w_packed ? 1 : 0;
+    a.bias = bias;
+    a.y = nullptr;
+    a.ldy = 0;
+    a.M = batch;
+    a.N = N;
+    a.K = K;
+    a.vec_y = 0;
+    a.part = nullptr;
+    a.counters = nullptr;
+    a.splits = 1;
+    a.epi = ls::GEMM_ROPE;
+    return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_qkv_rope_write");
 }
 
 size_t ls_decode_gemm_workspace_bytes(int M, int N, int K) {
@@ -836,15 +906,14 @@ size_t ls_decode_gemm_workspace_bytes(int M, int N, int K) {
 }
 
 int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
-                   const void* bias, void* y, int64_t y_stride, int M, int N, int K,
+                   int w_packed, const void* bias, void* y, int64_t y_stride, int M, int N, int K,
                    void* workspace, size_t workspace_bytes, void* stream) {
     if (!x || !w || !y) return fail(LS_ERR_INVALID, "null pointer argument");
     if (M < 0 || M > ls::GEMM_MAX_M || N < 0 || K < 32 || K % 32 != 0)
         return fail(LS_ERR_INVALID,
                     "need 0 <= M <= %d, N >= 0, K a positive multiple of 32 (M %d, N %d, K %d)",
                     ls::GEMM_MAX_M, M, N, K);
-    if (!aligned(x, 16) || !aligned(w, 16) || x_stride % 8 != 0 || w_stride % 8 != 0 ||
-        x_stride < K || w_stride < K)
+    if (!weight_ok(x, x_stride, w, w_stride, w_packed, K))
         return fail(LS_ERR_INVALID, "x and w rows must be 16-byte aligned and hold K values");
     if (!aligned(y, 2) || (M > 1 && y_stride < N))
         return fail(LS_ERR_INVALID, "y must be 2-byte aligned with y_stride >= N");
@@ -854,6 +923,7 @@ int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_str
     a.ldx = x_stride;
     a.w = w;
     a.ldw = w_stride;
+    a.w_packed = w_packed ? 1 : 0;
     a.bias = bias;
     a.y = y;
     a.ldy = y_stride;
@@ -864,7 +934,7 @@ int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_str
     a.splits = M > 0 && N > 0 ? ls::decode_gemm_splits(M, N, K) : 1;
     a.part = (float*)workspace;
     a.counters = nullptr;
-    a.glu = 0;
+    a.epi = ls::GEMM_PLAIN;
     if (a.splits > 1) {
         const size_t need = ls::decode_gemm_workspace_bytes(M, N, K);
         if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
@@ -880,15 +950,14 @@ int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_str
 }
 
 int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
-                           const void* bias, void* y, int64_t y_stride, int M, int inter, int K,
-                           void* stream) {
+                           int w_packed, const void* bias, void* y, int64_t y_stride, int M,
+                           int inter, int K, void* stream) {
     if (!x || !w || !y) return fail(LS_ERR_INVALID, "null pointer argument");
     if (M < 0 || M > ls::GEMM_MAX_M || inter < 0 || inter > (1 << 29) || K < 32 || K % 32 != 0)
         return fail(LS_ERR_INVALID,
                     "need 0 <= M <= %d, inter >= 0, K a positive multiple of 32 (M %d, inter %d, "
                     "K %d)", ls::GEMM_MAX_M, M, inter, K);
-    if (!aligned(x, 16) || !aligned(w, 16) || x_stride % 8 != 0 || w_stride % 8 != 0 ||
-        x_stride < K || w_stride < K)
+    if (!weight_ok(x, x_stride, w, w_stride, w_packed, K))
         return fail(LS_ERR_INVALID, "x and w rows must be 16-byte aligned and hold K values");
     if (!aligned(y, 2) || (M > 1 && y_stride < inter))
         return fail(LS_ERR_INVALID, "y must be 2-byte aligned with y_stride >= inter");
@@ -902,6 +971,7 @@ int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64
     a.ldx = x_stride;
     a.w = w;
     a.ldw = w_stride;
+    a.w_packed = w_packed ? 1 : 0;
     a.bias = bias;
     a.y = y;
     a.ldy = y_stride;
@@ -912,7 +982,7 @@ int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64
     a.part = nullptr;
     a.counters = nullptr;
     a.splits = 1;
-    a.glu = 1;
+    a.epi = ls::GEMM_GLU;
     return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_gate_up_silu");
 }
 
@@ -922,6 +992,28 @@ int ls_compute_probe(int mode, int groups, int items, float scale, float* out, v
         return fail(LS_ERR_INVALID, "mode 0 or 1, groups in [1, 65535], items >= 1");
     return hip_status(ls::launch_compute_probe(mode, groups, items, scale, out, (hipStream_t)stream),
                       "ls_compute_probe");
+}
+
+size_t ls_gemm_packed_bytes(int N, int K, int kind, int head_dim) {
+    if (N < 1 || K < 32 || K % 32 != 0 || kind < 0 || kind > 2) return 0;
+    return ls::gemm_packed_bytes(N, K, kind, head_dim);
+}
+
+int ls_pack_gemm_weight(const void* w, int64_t w_stride, int N, int K, int kind, int head_dim,
+                        void* packed, void* stream) {
+    if (!w || !packed) return fail(LS_ERR_INVALID, "null pointer argument");
+    if (N < 1 || K < 32 || K % 32 != 0)
+        return fail(LS_ERR_INVALID, "need N >= 1 and K a positive multiple of 32 (N %d, K %d)", N,
+                    K);
+    if (kind < 0 || kind > 2) return fail(LS_ERR_INVALID, "kind must be 0, 1 or 2, got %d", kind);
+    if (kind == 1 && N % 2 != 0) return fail(LS_ERR_INVALID, "a gate/up weight has 2I rows");
+    if (kind == 2 && (head_dim < 16 || head_dim % 16 != 0 || N % head_dim != 0))
+        return fail(LS_ERR_INVALID, "a q/k/v weight needs head_dim % 16 == 0 dividing N");
+    if (!aligned(w, 16) || w_stride % 8 != 0 || w_stride < K || !aligned(packed, 16))
+        return fail(LS_ERR_INVALID, "w rows and packed must be 16-byte aligned");
+    return hip_status(ls::launch_pack_gemm_weight(w, w_stride, N, K, kind, head_dim, packed,
+                                                  (hipStream_t)stream),
+                      "ls_pack_gemm_weight");
 }
 
 }  // extern "C"

@@ -88,4 +88,14 @@ __device__ __forceinline__ _Float16 silu_mul_h(_Float16 g, _Float16 u) {
     return (_Float16)((float)sg * (float)u);
 }
 
+// One RoPE output as Hugging Face's fp16 apply_rotary_pos_emb rounds it:
+// fp16(fp16(x * c) + fp16(y * s)), y the rotate-half partner (negated for
+// the first half).  Shared, so every kernel that rotates is bit-equal.
+__device__ __forceinline__ _Float16 rope_h(_Float16 x, _Float16 c, _Float16 y, _Float16 s) {
+#pragma clang fp contract(off)
+    const _Float16 xc = (_Float16)((float)x * (float)c);
+    const _Float16 ys = (_Float16)((float)y * (float)s);
+    return (_Float16)((float)xc + (float)ys);
+}
+
 }  // namespace ls

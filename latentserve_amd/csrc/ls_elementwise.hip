@@ -27,11 +27,6 @@ namespace {
 __device__ __forceinline__ float f(half_t h) { return (float)h; }
 __device__ __forceinline__ half_t hf(float v) { return (half_t)v; }
 
-// Two fp16 products rounded, then their sum rounded: Hugging Face's
-// (x * cos) + (rotate_half(x) * sin) for one element.
-__device__ __forceinline__ half_t rope1(half_t x, half_t c, half_t y, half_t s) {
-    return hf(f(hf(f(x) * f(c))) + f(hf(f(y) * f(s))));
-}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -193,8 +188,8 @@ __global__ __launch_bounds__(512) void rope_qk_kernel(RopeParams a) {
     const half_t* c = (const half_t*)a.cos + r * a.sc;
     const half_t* s = (const half_t*)a.sin + r * a.ss;
     const half_t x0 = src[i], x1 = src[i + hd];
-    dst[i] = rope1(x0, c[i], -x1, s[i]);
-    dst[i + hd] = rope1(x1, c[i + hd], x0, s[i + hd]);
+    dst[i] = rope_h(x0, c[i], -x1, s[i]);
+    dst[i + hd] = rope_h(x1, c[i + hd], x0, s[i + hd]);
 }
 
 // grid (hq + 2 hk, B), d / 2 threads.  Heads [0, hq) are queries, then hk
@@ -212,8 +207,8 @@ __global__ __launch_bounds__(512) void rope_write_decode_kernel(RopeWriteParams 
         const int n_rep = a.hq / a.hk;
         half_t* dst = (half_t*)a.q_out + b * a.sq_b + (int64_t)(j / n_rep) * a.sq_h +
                       (int64_t)(j % n_rep) * a.sq_r;
-        dst[i] = rope1(x0, c[i], -x1, s[i]);
-        dst[i + hd] = rope1(x1, c[i + hd], x0, s[i + hd]);
+        dst[i] = rope_h(x0, c[i], -x1, s[i]);
+        dst[i + hd] = rope_h(x1, c[i + hd], x0, s[i + hd]);
         return;
     }
     const int64_t slot = a.slots[b];
@@ -225,8 +220,8 @@ __global__ __launch_bounds__(512) void rope_write_decode_kernel(RopeWriteParams 
     half_t* dst = (half_t*)(isk ? a.k_pool : a.v_pool) + blk * a.sp_b + off * a.sp_t +
                   (int64_t)h * a.sp_h;
     if (isk) {
-        const half_t k0 = rope1(x0, c[i], -x1, s[i]);
-        const half_t k1 = rope1(x1, c[i + hd], x0, s[i + hd]);
+        const half_t k0 = rope_h(x0, c[i], -x1, s[i]);
+        const half_t k1 = rope_h(x1, c[i + hd], x0, s[i + hd]);
         dst[i] = k0;
         dst[i + hd] = k1;
         if (a.kmin) {

@@ -5,13 +5,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ls_elementwise.h"
+
 namespace ls {
 
 struct GemmParams {
     const void* x;       // fp16 [M, K], row stride ldx
     int64_t ldx;
-    const void* w;       // fp16 [N, K], row stride ldw (a torch Linear weight)
-    int64_t ldw;
+    const void* w;       // fp16 [N, K], row stride ldw (a torch Linear weight), or
+    int64_t ldw;         // packed (w_packed): see gemm_packed_bytes
+    int w_packed;
     const void* bias;    // fp16 [N] or NULL
     void* y;             // fp16 [M, N], row stride ldy
     int64_t ldy;
@@ -20,11 +23,25 @@ struct GemmParams {
     float* part;         // fp32 partial sums [splits][M][ldp] when splits > 1
     unsigned* counters;  // arrivals a tile group, zero on entry and on exit
     int splits;          // workgroups a 16-row tile's K is split over
-    int glu;             // 1: y[M, N/2] = silu(gate) * up of w = [gate; up]
+    int epi;             // GEMM_PLAIN, GEMM_GLU: y[M, N/2] = silu(gate) * up of w =
+                         // [gate; up], GEMM_ROPE: the fused q/k/v projection's outputs
+                         // rotated and stored as `rope` describes (y unused)
+    RopeWriteParams rope;
 };
+
+enum GemmEpilogue { GEMM_PLAIN = 0, GEMM_GLU = 1, GEMM_ROPE = 2 };
 
 // Largest M one launch takes (four 16-row column blocks of the MFMA tile).
 constexpr int GEMM_MAX_M = 64;
+
+// Packed weights: the 16-row tiles of an epilogue's row mapping, each
+// 32-channel step of a tile 1 KiB in the order the lanes load it (lane
+// (r, g) holds row r's channels 8g .. 8g + 7 of the step), tiles padded to a
+// multiple of 4 with zero rows.  Every weight load of a packed launch reads
+// 1 KiB contiguous.  Bytes of the packed form of an [N, K] weight:
+size_t gemm_packed_bytes(int N, int K, int epi, int head_dim);
+hipError_t launch_pack_gemm_weight(const void* w, int64_t ldw, int N, int K, int epi, int head_dim,
+                                   void* packed, hipStream_t stream);
 
 // Splits of K over workgroups for an [M, N, K] product (1: no workspace).
 int decode_gemm_splits(int M, int N, int K);

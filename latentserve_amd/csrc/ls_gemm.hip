@@ -36,9 +36,16 @@
 // launches it replaces round it (fp16 gate and up, then the fp16 SiLU
 // product), so the fused and separate paths are bit-equal.
 //
+// The fused q/k/v form pairs each head's channel with its rotate-half
+// partner the same way and finishes as ls_rope_write_decode: RoPE, the
+// query folded to [B, H_kv, n_rep, D], the key and value stored at the
+// sequence's slot (with the page K bounds), bit-equal to the two launches.
+//
 // The reference runs these projections as torch (cuBLAS) GEMMs inside its
-// model layers (model/fused.py, model/latentserve_qwen.py) and the
-// activation as silu_and_mul (kernels/fused_elementwise.py:222-233).
+// model layers (model/fused.py, model/latentserve_qwen.py), the activation
+// as silu_and_mul (kernels/fused_elementwise.py:222-233) and the decode
+// token's rope_qk and cache write in its attention layer
+// (model/attention/gqa.py:251-253, cache/paged_cache.py write).
 #include "ls_common.h"
 #include "ls_gemm.h"
 
@@ -74,24 +81,125 @@ __device__ __forceinline__ void store_out(const GemmParams& a, int m, int nc, in
 
 // W row of output-tile row r: plain tiles hold 16 consecutive rows; gate/up
 // tiles hold gate rows 8T .. 8T + 7 and the up rows I + 8T .. (rows past the
-// edge clamped to a valid one: their outputs are not stored).
-template <bool GLU>
-__device__ __forceinline__ int w_row(const GemmParams& a, int tile, int r) {
-    if (GLU) {
-        const int half_n = a.N / 2, j0 = 8 * tile + (r & 7), j = j0 < half_n ? j0 : half_n - 1;
+// edge clamped to a valid one: their outputs are not stored); RoPE tiles
+// hold 8 channels of a head's first half and their rotate-half partners,
+// head T / (d / 16), channels 8 (T % (d / 16)) + [0, 8) and + d / 2.
+template <int EPI>
+__device__ __forceinline__ int w_row_of(int N, int d, int tile, int r, bool& real) {
+    if (EPI == GEMM_GLU) {
+        const int half_n = N / 2, j0 = 8 * tile + (r & 7), j = j0 < half_n ? j0 : half_n - 1;
+        real = j0 < half_n;
         return r < 8 ? j : half_n + j;
     }
-    const int n = 16 * tile + r;
-    return n < a.N ? n : a.N - 1;
+    int n;
+    if (EPI == GEMM_ROPE) {
+        const int tph = d / 16, head = tile / tph, i = 8 * (tile % tph) + (r & 7);
+        n = head * d + i + (r < 8 ? 0 : d / 2);
+    } else {
+        n = 16 * tile + r;
+    }
+    real = n < N;
+    return n < N ? n : N - 1;
+}
+template <int EPI>
+__device__ __forceinline__ int w_row(const GemmParams& a, int tile, int r) {
+    bool real;
+    return w_row_of<EPI>(a.N, a.rope.d, tile, r, real);
+}
+
+// Packed weights (gemm_packed_bytes): tile T's step s is 64 lanes x 16 B at
+// ((T * steps + s) * 64 + lane) * 8 halves.
+constexpr int GEMM_PACK_TILES = 4;    // tiles padded to a multiple of the largest TPW
+
+// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding).
+constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// LDS rows of a wave's X chunk (one column block, 16 steps): 16 rows of 512
+// channels, padded by 16 bytes so the rows of a 16-lane read fall in
+// different banks.
+constexpr int XROW_BYTES = 16 * 64 + 16;
+constexpr int XREG_BYTES = 16 * XROW_BYTES;
+
+// The fused q/k/v projection's epilogue for one lane: channels i .. i + 3
+// of head `head` (i < d / 2) and their partners i + d / 2 .. for sequence
+// m, as x0 / x1 (fp16, bias added); rotated and stored as
+// rope_write_decode_kernel stores them (the same rounding, bit-equal).
+__device__ __forceinline__ void rope_store(const RopeWriteParams& a, int m, int head, int i,
+                                           const half_t* x0, const half_t* x1) {
+    const int hd = a.d / 2;
+    int64_t p = a.pos[m];
+    p = p < 0 ? 0 : (p >= a.tab_rows ? a.tab_rows - 1 : p);
+    const half_t* c = (const half_t*)a.cos + p * a.st;
+    const half_t* s = (const half_t*)a.sin + p * a.st;
+    half_t o0[4], o1[4];
+    if (head < a.hq + a.hk) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            o0[e] = rope_h(x0[e], c[i + e], -x1[e], s[i + e]);
+            o1[e] = rope_h(x1[e], c[i + hd + e], x0[e], s[i + hd + e]);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            o0[e] = x0[e];
+            o1[e] = x1[e];
+        }
+    }
+    half_t* dst;
+    if (head < a.hq) {
+        const int n_rep = a.hq / a.hk;
+        dst = (half_t*)a.q_out + (int64_t)m * a.sq_b + (int64_t)(head / n_rep) * a.sq_h +
+              (int64_t)(head % n_rep) * a.sq_r;
+    } else {
+        const int64_t slot = a.slots[m];
+        if (slot < 0) return;
+        const int64_t blk = slot / a.page, off = slot % a.page;
+        if (blk >= a.num_blocks) return;
+        const bool isk = head < a.hq + a.hk;
+        const int h = isk ? head - a.hq : head - a.hq - a.hk;
+        dst = (half_t*)(isk ? a.k_pool : a.v_pool) + blk * a.sp_b + off * a.sp_t +
+              (int64_t)h * a.sp_h;
+        if (isk && a.kmin) {
+            // the page's K bounds: its first token resets them (fp16 min /
+            // max are exact)
+            half_t* mn = (half_t*)a.kmin + blk * a.sb_b + (int64_t)h * a.sb_h;
+            half_t* mx = (half_t*)a.kmax + blk * a.sb_b + (int64_t)h * a.sb_h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (off == 0) {
+                    mn[i + e] = o0[e];
+                    mx[i + e] = o0[e];
+                    mn[i + hd + e] = o1[e];
+                    mx[i + hd + e] = o1[e];
+                } else {
+                    mn[i + e] = (half_t)fminf((float)mn[i + e], (float)o0[e]);
+                    mx[i + e] = (half_t)fmaxf((float)mx[i + e], (float)o0[e]);
+                    mn[i + hd + e] = (half_t)fminf((float)mn[i + hd + e], (float)o1[e]);
+                    mx[i + hd + e] = (half_t)fmaxf((float)mx[i + hd + e], (float)o1[e]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        dst[i + e] = o0[e];
+        dst[i + hd + e] = o1[e];
+    }
 }
 
 // One workgroup a (TPW tiles, split); its blockDim.x / 64 waves take
 // consecutive K chunks of the split's range.  MB column blocks of 16 rows
 // of X.  The waves' tiles are summed through LDS (blockDim.x / 64 * TPW *
 // MB KiB of dynamic shared memory).
-template <int SPW, int TPW, int MB, bool GLU>
+// PW: the weight is packed.  LX (one column block of 16-step chunks): the
+// wave's X chunk is brought to its own LDS rows by direct loads (1 KiB of
+// one row each) and read from there in MFMA order; the same LDS then holds
+// the wave's partial tiles for the group's sum.  (X loaded straight to
+// registers reads 64 bytes of each of 16 rows per instruction.)
+template <int SPW, int TPW, int MB, int EPI, bool PW, bool LX>
 __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
-    extern __shared__ f4 red[];                       // [waves][TPW][MB][WAVE]
+    static_assert(!LX || (MB == 1 && SPW == 16), "LDS X: one column block, 16-step chunks");
+    extern __shared__ f4 red[];                       // [waves][TPW][MB][WAVE] (LX: per wave)
     const int nw = blockDim.x / WAVE;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
     const int r = lane & 15, g = lane >> 4;
@@ -111,25 +219,56 @@ __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
     // which stream through two register sets: tile t + 2 is issued once
     // tile t is consumed, so one tile is always in flight behind the one
     // being summed.
-    u4 xb[SPW][MB];
+    u4 xb[LX ? 1 : SPW][MB];
     u4 wb[2][SPW];
+    char* const xl = (char*)red + wv * XREG_BYTES;    // LX: this wave's X rows
     auto load_w = [&](int b, int t) {
-        const half_t* wp = (const half_t*)a.w + (int64_t)w_row<GLU>(a, tile0 + t, r) * a.ldw +
-                           32 * s0 + 8 * g;
+        const half_t* wp;
+        int step_halves;
+        if (PW) {
+            wp = (const half_t*)a.w + (((int64_t)(tile0 + t) * steps + s0) * WAVE + lane) * 8;
+            step_halves = WAVE * 8;
+        } else {
+            wp = (const half_t*)a.w + (int64_t)w_row<EPI>(a, tile0 + t, r) * a.ldw + 32 * s0 +
+                 8 * g;
+            step_halves = 32;
+        }
 #pragma unroll
         for (int i = 0; i < SPW; ++i) {
             const int st = i < last ? i : last;
-            wb[b][i] = *(const u4*)(wp + 32 * st);
+            wb[b][i] = *(const u4*)(wp + step_halves * st);
         }
     };
+    if constexpr (LX) {
+        // row q's 512 channels of the chunk: lane l brings channels 8l ..
+        // 8l + 7 (a chunk shorter than 16 steps reads clamped channels whose
+        // steps are masked)
+        const int col = 32 * s0 + 8 * lane < a.K - 8 ? 32 * s0 + 8 * lane : a.K - 8;
 #pragma unroll
-    for (int i = 0; i < SPW; ++i) {
-        const int st = i < last ? i : last;
+        for (int q = 0; q < 16; ++q) {
+            const int m = q < a.M ? q : a.M - 1;
+            __builtin_amdgcn_global_load_lds(
+                (const void*)((const half_t*)a.x + (int64_t)m * a.ldx + col),
+                (__attribute__((address_space(3))) void*)(xl + q * XROW_BYTES), 16, 0, 0);
+        }
+    } else {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) xb[i][mb] = *(const u4*)(xp[mb] + 32 * st);
+        for (int i = 0; i < SPW; ++i) {
+            const int st = i < last ? i : last;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) xb[i][mb] = *(const u4*)(xp[mb] + 32 * st);
+        }
     }
     load_w(0, 0);
     if (TPW > 1) load_w(1, 1);
+    if constexpr (LX) {
+        // the X rows were requested before every weight load: once no more
+        // than the weight loads are outstanding, they are in LDS
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(SPW * (TPW > 1 ? 2 : 1)));
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    }
     f4 acc[TPW][MB];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
@@ -145,7 +284,11 @@ __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
             const u4 w = wb[t & 1][i];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
-                const u4 xv = live ? xb[i][mb] : z;
+                u4 xv;
+                if constexpr (LX)
+                    xv = live ? *(const u4*)(xl + r * XROW_BYTES + (32 * i + 8 * g) * 2) : z;
+                else
+                    xv = live ? xb[i][mb] : z;
                 acc[t][mb] = mfma16(as_h4(w.x, w.y), as_h4(xv.x, xv.y), acc[t][mb]);
                 acc[t][mb] = mfma16(as_h4(w.z, w.w), as_h4(xv.z, xv.w), acc[t][mb]);
             }
@@ -157,23 +300,56 @@ __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
     }
 
     if (nw > 1) {
+        // wave p's partials: its own X rows when LX (another wave may still
+        // be reading its own), else slot p
+        auto slot = [&](int p) {
+            return LX ? (f4*)((char*)red + p * XREG_BYTES) : red + p * TPW * MB * WAVE;
+        };
 #pragma unroll
         for (int t = 0; t < TPW; ++t)
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-                red[((wv * TPW + t) * MB + mb) * WAVE + lane] = acc[t][mb];
+            for (int mb = 0; mb < MB; ++mb) slot(wv)[(t * MB + mb) * WAVE + lane] = acc[t][mb];
         __syncthreads();
         if (wv != 0) return;
         for (int p = 1; p < nw; ++p)
 #pragma unroll
             for (int t = 0; t < TPW; ++t)
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb)
-                    acc[t][mb] += red[((p * TPW + t) * MB + mb) * WAVE + lane];
+                for (int mb = 0; mb < MB; ++mb) acc[t][mb] += slot(p)[(t * MB + mb) * WAVE + lane];
     }
     // wave 0 alone from here
 
-    if (GLU) {
+    if (EPI == GEMM_ROPE) {
+        // splits == 1 (host): lanes g = 0, 1 hold channels 8t + 4g + e of the
+        // tile's head, lanes g + 2 their rotate-half partners
+        const int tph = a.rope.d / 16;
+#pragma unroll
+        for (int t = 0; t < TPW; ++t)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                f4 up;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) up[e] = __shfl_xor(acc[t][mb][e], 32);
+                const int tile = tile0 + t, head = tile / tph, i = 8 * (tile % tph) + 4 * g;
+                const int m = 16 * mb + r;
+                if (g >= 2 || m >= a.M || head >= a.rope.hq + 2 * a.rope.hk) continue;
+                const int n0 = head * a.rope.d + i, n1 = n0 + a.rope.d / 2;
+                half_t x0[4], x1[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v0 = acc[t][mb][e], v1 = up[e];
+                    if (a.bias) {
+                        v0 += (float)((const half_t*)a.bias)[n0 + e];
+                        v1 += (float)((const half_t*)a.bias)[n1 + e];
+                    }
+                    x0[e] = (half_t)v0;
+                    x1[e] = (half_t)v1;
+                }
+                rope_store(a.rope, m, head, i, x0, x1);
+            }
+        return;
+    }
+    if (EPI == GEMM_GLU) {
         // splits == 1 (host): lanes g = 0, 1 hold gate columns 8T + 4g + e,
         // lanes g + 2 the matching up columns
         const int half_n = a.N / 2;
@@ -318,27 +494,37 @@ GemmShape gemm_shape(int M, int N, int K) {
     return s;
 }
 
-template <int TPW, int MB, bool GLU>
+template <int TPW, int MB, int EPI>
 void launch_kernel(const GemmParams& p, const GemmShape& sh, hipStream_t stream) {
     const dim3 grid(sh.units, p.splits), block(WAVE * sh.group_waves);
+    if (p.w_packed && MB == 1) {
+        const size_t lds = (size_t)sh.group_waves * XREG_BYTES;
+        hipLaunchKernelGGL((decode_gemm_kernel<spw_for(MB), TPW, MB, EPI, true, MB == 1>), grid,
+                           block, lds, stream, p);
+        return;
+    }
     const size_t lds =
         sh.group_waves > 1 ? (size_t)sh.group_waves * TPW * MB * WAVE * sizeof(f4) : 0;
-    hipLaunchKernelGGL((decode_gemm_kernel<spw_for(MB), TPW, MB, GLU>), grid, block, lds, stream,
-                       p);
+    if (p.w_packed)
+        hipLaunchKernelGGL((decode_gemm_kernel<spw_for(MB), TPW, MB, EPI, true, false>), grid,
+                           block, lds, stream, p);
+    else
+        hipLaunchKernelGGL((decode_gemm_kernel<spw_for(MB), TPW, MB, EPI, false, false>), grid,
+                           block, lds, stream, p);
 }
 
-template <bool GLU>
+template <int EPI>
 void launch_any(const GemmParams& p, const GemmShape& sh, hipStream_t stream) {
     if (sh.mb == 1 && sh.tpw == 4)
-        launch_kernel<4, 1, GLU>(p, sh, stream);
+        launch_kernel<4, 1, EPI>(p, sh, stream);
     else if (sh.mb == 1 && sh.tpw == 2)
-        launch_kernel<2, 1, GLU>(p, sh, stream);
+        launch_kernel<2, 1, EPI>(p, sh, stream);
     else if (sh.mb == 1)
-        launch_kernel<1, 1, GLU>(p, sh, stream);
+        launch_kernel<1, 1, EPI>(p, sh, stream);
     else if (sh.mb == 2)
-        launch_kernel<1, 2, GLU>(p, sh, stream);
+        launch_kernel<1, 2, EPI>(p, sh, stream);
     else
-        launch_kernel<1, 4, GLU>(p, sh, stream);
+        launch_kernel<1, 4, EPI>(p, sh, stream);
 }
 
 }  // namespace
@@ -346,6 +532,49 @@ void launch_any(const GemmParams& p, const GemmShape& sh, hipStream_t stream) {
 int decode_gemm_splits(int M, int N, int K) { return gemm_shape(M, N, K).splits; }
 
 int decode_gemm_units(int M, int N, int K) { return gemm_shape(M, N, K).units; }
+
+namespace {
+
+// grid (padded tiles, steps), 64 threads: lane (r, g) copies row r's
+// channels 8g .. 8g + 7 of the step (zeros for rows past the weight).
+template <int EPI>
+__global__ __launch_bounds__(64) void pack_gemm_kernel(const half_t* w, int64_t ldw, int N, int K,
+                                                       int d, half_t* out) {
+    const int T = blockIdx.x, s = blockIdx.y, lane = threadIdx.x, r = lane & 15, g = lane >> 4;
+    const int steps = K / 32;
+    bool real;
+    const int row = w_row_of<EPI>(N, d, T, r, real);
+    u4 v = {0u, 0u, 0u, 0u};
+    if (real) v = *(const u4*)(w + (int64_t)row * ldw + 32 * s + 8 * g);
+    *(u4*)(out + (((int64_t)T * steps + s) * WAVE + lane) * 8) = v;
+}
+
+}  // namespace
+
+size_t gemm_packed_bytes(int N, int K, int epi, int head_dim) {
+    (void)epi;
+    (void)head_dim;
+    const int tiles = (N + 15) / 16;
+    const int padded = (tiles + GEMM_PACK_TILES - 1) / GEMM_PACK_TILES * GEMM_PACK_TILES;
+    return (size_t)padded * (K / 32) * WAVE * 16;
+}
+
+hipError_t launch_pack_gemm_weight(const void* w, int64_t ldw, int N, int K, int epi, int head_dim,
+                                   void* packed, hipStream_t stream) {
+    const int tiles = (N + 15) / 16;
+    const int padded = (tiles + GEMM_PACK_TILES - 1) / GEMM_PACK_TILES * GEMM_PACK_TILES;
+    const dim3 grid(padded, K / 32);
+    if (epi == GEMM_GLU)
+        hipLaunchKernelGGL(pack_gemm_kernel<GEMM_GLU>, grid, dim3(WAVE), 0, stream,
+                           (const half_t*)w, ldw, N, K, head_dim, (half_t*)packed);
+    else if (epi == GEMM_ROPE)
+        hipLaunchKernelGGL(pack_gemm_kernel<GEMM_ROPE>, grid, dim3(WAVE), 0, stream,
+                           (const half_t*)w, ldw, N, K, head_dim, (half_t*)packed);
+    else
+        hipLaunchKernelGGL(pack_gemm_kernel<GEMM_PLAIN>, grid, dim3(WAVE), 0, stream,
+                           (const half_t*)w, ldw, N, K, head_dim, (half_t*)packed);
+    return hipGetLastError();
+}
 
 size_t decode_gemm_workspace_bytes(int M, int N, int K) {
     const GemmShape sh = gemm_shape(M, N, K);
@@ -357,11 +586,14 @@ hipError_t launch_decode_gemm(const GemmParams& p, hipStream_t stream) {
     if (p.M == 0 || p.N == 0) return hipSuccess;
     const GemmShape sh = gemm_shape(p.M, p.N, p.K);
     if (sh.splits != p.splits || sh.group_waves > MAX_GROUP_WAVES) return hipErrorInvalidValue;
-    if (p.glu) {
+    if (p.epi == GEMM_GLU) {
         if (p.splits != 1 || p.N % 2 != 0) return hipErrorInvalidValue;
-        launch_any<true>(p, sh, stream);
+        launch_any<GEMM_GLU>(p, sh, stream);
+    } else if (p.epi == GEMM_ROPE) {
+        if (p.splits != 1 || p.N % 16 != 0 || p.rope.d % 16 != 0) return hipErrorInvalidValue;
+        launch_any<GEMM_ROPE>(p, sh, stream);
     } else {
-        launch_any<false>(p, sh, stream);
+        launch_any<GEMM_PLAIN>(p, sh, stream);
     }
     return hipGetLastError();
 }

@@ -3,7 +3,10 @@
 ``gate_up_silu(x, weight)`` is the MLP's gate/up projection with
 silu_and_mul (kernels/fused_elementwise.py:222-233) in the GEMM's
 epilogue: one launch, bit-equal to ``linear`` followed by the separate
-activation kernel.
+activation kernel.  ``qkv_rope_write(x, w_qkv, bias, ...)`` is the attention
+layer's fused q/k/v projection finished in its epilogue exactly as
+``fused_elementwise.rope_write_decode`` finishes it (RoPE, the query fold,
+the K/V store and page bounds): one launch, bit-equal to the two.
 
 ``linear(x, weight, bias)`` computes what torch.nn.functional.linear does
 for fp16 operands (x [..., K], weight [N, K] as a torch Linear holds it),
@@ -58,8 +61,51 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
-def supports(x: torch.Tensor, weight: torch.Tensor) -> bool:
+KINDS = {"plain": 0, "gate_up": 1, "qkv": 2}
+
+
+class PackedWeight:
+    """A projection weight [N, K] packed for its launch kind (ls_pack_gemm_weight):
+    every weight load then reads 1 KiB contiguous.  ``kind``: "plain" for
+    linear, "gate_up" for gate_up_silu, "qkv" for qkv_rope_write (with the
+    head width)."""
+
+    def __init__(self, weight: torch.Tensor, kind: str = "plain", head_dim: int = 128):
+        if not weight.is_cuda or weight.dtype != torch.float16 or weight.dim() != 2:
+            raise ValueError("weight must be a 2-D fp16 GPU tensor")
+        if weight.stride(-1) != 1 or weight.stride(0) % 8 or weight.data_ptr() % 16:
+            weight = weight.contiguous()
+        n, k = weight.shape
+        nbytes = int(_lib.lib().ls_gemm_packed_bytes(n, k, KINDS[kind], head_dim))
+        if nbytes == 0:
+            raise ValueError(f"cannot pack a [{n}, {k}] weight (K must be a multiple of 32)")
+        self.data = torch.empty(nbytes // 2, dtype=torch.float16, device=weight.device)
+        rc = _lib.lib().ls_pack_gemm_weight(weight.data_ptr(), weight.stride(0), n, k,
+                                            KINDS[kind], head_dim, self.data.data_ptr(),
+                                            torch.cuda.current_stream(weight.device).cuda_stream)
+        _lib.check(rc, "ls_pack_gemm_weight")
+        self.shape = (n, k)
+        self.kind = kind
+        self.head_dim = head_dim
+        self.device = weight.device
+        self.dtype = weight.dtype
+
+
+def _weight_args(weight, kind: str):
+    """(pointer, row stride, packed flag, [N, K]) of a tensor or PackedWeight."""
+    if isinstance(weight, PackedWeight):
+        if weight.kind != kind:
+            raise ValueError(f"weight packed for {weight.kind!r}, used for {kind!r}")
+        return weight.data.data_ptr(), 0, 1, weight.shape
+    return weight.data_ptr(), weight.stride(0), 0, tuple(weight.shape)
+
+
+def supports(x: torch.Tensor, weight) -> bool:
     """Whether ``linear`` takes these operands without a copy."""
+    if isinstance(weight, PackedWeight):
+        rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
+        return (x.is_cuda and x.dtype == torch.float16 and rows <= MAX_ROWS
+                and x.shape[-1] == weight.shape[1] and x.shape[-1] % 32 == 0)
     rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
     return (x.is_cuda and weight.is_cuda and x.dtype == weight.dtype == torch.float16
             and rows <= MAX_ROWS and x.shape[-1] % 32 == 0 and weight.dim() == 2
@@ -71,13 +117,14 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
            out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y = x . weight^T (+ bias) for x [..., K] fp16 with at most 64 rows."""
     for name, t in (("x", x), ("weight", weight)):
-        if not t.is_cuda:
+        if not t.device.type == "cuda":
             raise ValueError(f"{name} must be on a GPU (the HIP kernels have no CPU path)")
         if t.dtype != torch.float16:
             raise ValueError(f"{name} must be float16, got {t.dtype}")
-    if weight.dim() != 2 or weight.shape[1] != x.shape[-1]:
-        raise ValueError(f"weight must be [N, {x.shape[-1]}], got {tuple(weight.shape)}")
-    n, k = weight.shape
+    wptr, wstride, packed, wshape = _weight_args(weight, "plain")
+    if len(wshape) != 2 or wshape[1] != x.shape[-1]:
+        raise ValueError(f"weight must be [N, {x.shape[-1]}], got {tuple(wshape)}")
+    n, k = wshape
     x2 = x.reshape(-1, k)
     if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) % 8) or x2.data_ptr() % 16:
         x2 = x2.contiguous()
@@ -93,7 +140,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     need = workspace_bytes(m, n, k)
     ws = _workspace(x.device, need) if need else None
     rc = _lib.lib().ls_decode_gemm(
-        x2.data_ptr(), x2.stride(0) if m > 1 else k, weight.data_ptr(), weight.stride(0),
+        x2.data_ptr(), x2.stride(0) if m > 1 else k, wptr, wstride, packed,
         None if bias is None else bias.data_ptr(), y.data_ptr(),
         y.stride(0) if m > 1 else n, m, n, k, None if ws is None else ws.data_ptr(), need,
         torch.cuda.current_stream(x.device).cuda_stream)
@@ -110,13 +157,14 @@ def gate_up_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Ten
     rounding)."""
     from latentserve_amd.kernels import fused_elementwise as fe
     for name, t in (("x", x), ("weight", weight)):
-        if not t.is_cuda:
+        if not t.device.type == "cuda":
             raise ValueError(f"{name} must be on a GPU (the HIP kernels have no CPU path)")
         if t.dtype != torch.float16:
             raise ValueError(f"{name} must be float16, got {t.dtype}")
-    if weight.dim() != 2 or weight.shape[1] != x.shape[-1] or weight.shape[0] % 2:
-        raise ValueError(f"weight must be [2I, {x.shape[-1]}], got {tuple(weight.shape)}")
-    n2, k = weight.shape
+    wptr, wstride, packed, wshape = _weight_args(weight, "gate_up")
+    if len(wshape) != 2 or wshape[1] != x.shape[-1] or wshape[0] % 2:
+        raise ValueError(f"weight must be [2I, {x.shape[-1]}], got {tuple(wshape)}")
+    n2, k = wshape
     inter = n2 // 2
     x2 = x.reshape(-1, k)
     if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) % 8) or x2.data_ptr() % 16:
@@ -125,6 +173,8 @@ def gate_up_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Ten
     if m > MAX_ROWS:
         raise ValueError(f"at most {MAX_ROWS} rows a call, got {m}")
     if m and inter and workspace_bytes(m, n2, k):
+        if packed:
+            raise ValueError("this K splits over workgroups: pass the row-major weight")
         return fe.silu_and_mul(linear(x, weight, bias), out=out)
     if bias is not None and (bias.shape != (n2,) or bias.dtype != torch.float16
                              or not bias.is_contiguous()):
@@ -134,9 +184,55 @@ def gate_up_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Ten
     if m == 0 or inter == 0:
         return y.view(*x.shape[:-1], inter)
     rc = _lib.lib().ls_decode_gate_up_silu(
-        x2.data_ptr(), x2.stride(0) if m > 1 else k, weight.data_ptr(), weight.stride(0),
+        x2.data_ptr(), x2.stride(0) if m > 1 else k, wptr, wstride, packed,
         None if bias is None else bias.data_ptr(), y.data_ptr(),
         y.stride(0) if m > 1 else inter, m, inter, k,
         torch.cuda.current_stream(x.device).cuda_stream)
     _lib.check(rc, "ls_decode_gate_up_silu")
     return y.view(*x.shape[:-1], inter)
+
+
+def qkv_rope_write(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                   positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                   slots: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, hq: int,
+                   hk: int, q_out: Optional[torch.Tensor] = None,
+                   kmin: Optional[torch.Tensor] = None,
+                   kmax: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """rope_write_decode(linear(x, weight, bias), ...) in one launch.
+
+    x [B, K] (or [B, 1, K]) fp16; weight [(hq + 2 hk) * D, K]; the rest as
+    fused_elementwise.rope_write_decode.  Returns q folded to [B, hk, hq //
+    hk, D] (q_out when given).  Where the GEMM would split K over
+    workgroups, the two launches run instead (same results)."""
+    from latentserve_amd.kernels import fused_elementwise as fe
+    for name, t in (("x", x), ("weight", weight)):
+        if not t.device.type == "cuda":
+            raise ValueError(f"{name} must be on a GPU (the HIP kernels have no CPU path)")
+        if t.dtype != torch.float16:
+            raise ValueError(f"{name} must be float16, got {t.dtype}")
+    wptr, wstride, packed, (n, k) = _weight_args(weight, "qkv")
+    b = x.shape[0]
+    x2 = x.reshape(b, k)
+    if x2.stride(-1) != 1 or (b > 1 and x2.stride(0) % 8) or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    d = cos.shape[-1]
+    two = (n != (hq + 2 * hk) * d or d % 16 or b > MAX_ROWS or not supports(x2, weight)
+           or (b and workspace_bytes(b, n, k)))
+    if two:
+        if packed:
+            raise ValueError("this shape takes two launches: pass the row-major weight")
+        return fe.rope_write_decode(linear(x2, weight, bias), positions, cos, sin, slots, k_pool,
+                                    v_pool, hq, hk, q_out=q_out, kmin=kmin, kmax=kmax)
+    if packed and weight.head_dim != d:
+        raise ValueError(f"weight packed for head_dim {weight.head_dim}, tables are {d} wide")
+    if bias is not None and (bias.shape != (n,) or bias.dtype != torch.float16
+                             or not bias.is_contiguous()):
+        raise ValueError(f"bias must be contiguous fp16 [{n}]")
+    args = fe.rope_write_args(positions, cos, sin, slots, k_pool, v_pool, hq, hk, b, d, q_out,
+                              kmin, kmax)
+    rc = _lib.lib().ls_decode_qkv_rope_write(
+        x2.data_ptr(), x2.stride(0) if b > 1 else k, wptr, wstride, packed,
+        None if bias is None else bias.data_ptr(), k, *args["pre"], b, hq, hk, d,
+        torch.cuda.current_stream(x.device).cuda_stream)
+    _lib.check(rc, "ls_decode_qkv_rope_write")
+    return args["q_out"]

@@ -195,14 +195,26 @@ def rope_write_decode(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Ten
     Positions past the table are clamped to its last row (the caller builds
     the tables to the cache's capacity).
     """
-    for name, t in (("qkv", qkv), ("cos", cos), ("sin", sin), ("k_pool", k_pool),
-                    ("v_pool", v_pool)):
-        _fp16_gpu(name, t)
+    _fp16_gpu("qkv", qkv)
     b = qkv.shape[0]
     d = cos.shape[-1]
     q2 = _rows(qkv.reshape(b, -1))
     if q2.shape[1] != (hq + 2 * hk) * d:
         raise ValueError(f"qkv rows must hold {(hq + 2 * hk) * d} values, got {q2.shape[1]}")
+    args = rope_write_args(positions, cos, sin, slots, k_pool, v_pool, hq, hk, b, d, q_out, kmin,
+                           kmax)
+    rc = _lib.lib().ls_rope_write_decode(q2.data_ptr(), _row_stride(q2), *args["pre"], b, hq, hk,
+                                         d, _stream(qkv))
+    _lib.check(rc, "ls_rope_write_decode")
+    return args["q_out"]
+
+
+def rope_write_args(positions, cos, sin, slots, k_pool, v_pool, hq: int, hk: int, b: int, d: int,
+                    q_out=None, kmin=None, kmax=None) -> dict:
+    """Checked C arguments shared by the decode-token writers: "pre" holds
+    positions .. bounds strides in ABI order, "q_out" the output."""
+    for name, t in (("cos", cos), ("sin", sin), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _fp16_gpu(name, t)
     pos = positions.reshape(b)
     sl = slots.reshape(b)
     for name, t in (("positions", pos), ("slots", sl)):
@@ -217,8 +229,8 @@ def rope_write_decode(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Ten
         raise ValueError(f"k_pool / v_pool must be matching [nb, page, {hk}, {d}] pools")
     n_rep = hq // hk
     if q_out is None:
-        q_out = torch.empty((b, hk, n_rep, d), dtype=qkv.dtype, device=qkv.device)
-    elif q_out.shape != (b, hk, n_rep, d) or q_out.stride(-1) != 1 or q_out.dtype != qkv.dtype:
+        q_out = torch.empty((b, hk, n_rep, d), dtype=torch.float16, device=k_pool.device)
+    elif q_out.shape != (b, hk, n_rep, d) or q_out.stride(-1) != 1 or q_out.dtype != torch.float16:
         raise ValueError(f"q_out must be fp16 [{b}, {hk}, {n_rep}, {d}] with unit last stride")
     bounds = None
     if kmin is not None:
@@ -227,14 +239,12 @@ def rope_write_decode(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Ten
                 or kmin.dtype != torch.float16 or kmax.dtype != torch.float16:
             raise ValueError("kmin / kmax must be matching fp16 [nb, hk, D] with unit last stride")
         bounds = _i64p(kmin.stride()[:2])
-    rc = _lib.lib().ls_rope_write_decode(
-        q2.data_ptr(), _row_stride(q2), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(),
-        cos.stride(0), cos.shape[0], sl.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
-        _i64p(k_pool.stride()[:3]), k_pool.shape[0], k_pool.shape[1], q_out.data_ptr(),
-        _i64p(q_out.stride()[:3]), None if kmin is None else kmin.data_ptr(),
-        None if kmax is None else kmax.data_ptr(), bounds, b, hq, hk, d, _stream(qkv))
-    _lib.check(rc, "ls_rope_write_decode")
-    return q_out
+    pre = (pos.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0],
+           sl.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), _i64p(k_pool.stride()[:3]),
+           k_pool.shape[0], k_pool.shape[1], q_out.data_ptr(), _i64p(q_out.stride()[:3]),
+           None if kmin is None else kmin.data_ptr(), None if kmax is None else kmax.data_ptr(),
+           bounds)
+    return {"pre": pre, "q_out": q_out}
 
 
 def embed_rms_norm(table: torch.Tensor, ids: torch.Tensor, weight: torch.Tensor, eps: float,

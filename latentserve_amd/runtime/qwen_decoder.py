@@ -9,8 +9,9 @@ vocab 151936, tied embeddings, RoPE theta 1e6, q/k/v biases) so a captured
 decode step can be timed on the reference's full-step configuration.  The
 projections run on the HIP weight-streaming GEMM up to 16 rows (hipBLASLt,
 through torch, above that, where it is faster), the MLP activation in the
-gate/up GEMM's epilogue; everything else is HIP as well: the embedding
-lookup inside the first norm, per layer the fused norms
+gate/up GEMM's epilogue and RoPE + the K/V store + the query fold in the
+q/k/v GEMM's; everything else is HIP as well: the embedding lookup inside
+the first norm, per layer the fused norms
 (residual add folded in), one launch for RoPE + the K/V store + the query
 fold (GQAAttention.forward's decode branch, model/attention/gqa.py:283-344:
 q [B, 12, 1, D] folded to [B, 2, 6, D], the new K/V written first), the
@@ -40,15 +41,23 @@ from latentserve_amd.runtime.kv_cache import KVCacheSpec, PagedKVCache
 HIP_GEMM_MAX_ROWS = 16
 
 
-def _linear(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None) -> torch.Tensor:
-    if x.shape[0] <= HIP_GEMM_MAX_ROWS and dg.supports(x, w):
-        return dg.linear(x, w, b)
+def _pack(w: torch.Tensor, kind: str, head_dim: int = 128):
+    """The weight packed for its HIP GEMM launch (GPU weights only)."""
+    return dg.PackedWeight(w, kind, head_dim) if w.is_cuda else None
+
+
+def _linear(x: torch.Tensor, w: torch.Tensor, pw=None,
+            b: Optional[torch.Tensor] = None) -> torch.Tensor:
+    wk = pw if pw is not None else w
+    if x.shape[0] <= HIP_GEMM_MAX_ROWS and dg.supports(x, wk):
+        return dg.linear(x, wk, b)
     return F.linear(x, w, b)
 
 
-def _gate_up_silu(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    if x.shape[0] <= HIP_GEMM_MAX_ROWS and dg.supports(x, w):
-        return dg.gate_up_silu(x, w)                 # SiLU in the GEMM's epilogue
+def _gate_up_silu(x: torch.Tensor, w: torch.Tensor, pw=None) -> torch.Tensor:
+    wk = pw if pw is not None else w
+    if x.shape[0] <= HIP_GEMM_MAX_ROWS and dg.supports(x, wk):
+        return dg.gate_up_silu(x, wk)                # SiLU in the GEMM's epilogue
     return fe.silu_and_mul(F.linear(x, w))
 
 
@@ -111,6 +120,11 @@ class _Layer:
         self.w_down = w(h, cfg.intermediate_size)
         self.norm1 = torch.ones(h, dtype=torch.float16, device=device)
         self.norm2 = torch.ones(h, dtype=torch.float16, device=device)
+        # packed copies for the decode GEMMs (every weight load 1 KiB contiguous)
+        self.p_qkv = _pack(self.w_qkv, "qkv", cfg.head_dim)
+        self.p_o = _pack(self.w_o, "plain")
+        self.p_gate_up = _pack(self.w_gate_up, "gate_up")
+        self.p_down = _pack(self.w_down, "plain")
 
 
 class QwenDecoder:
@@ -128,6 +142,7 @@ class QwenDecoder:
         self.lm_head = self.embed if cfg.tie_word_embeddings else (
             torch.randn(cfg.vocab_size, cfg.hidden_size, generator=gen, device=self.device)
             * std).to(torch.float16)
+        self.p_lm_head = _pack(self.lm_head, "plain")
         self.cache: Optional[PagedKVCache] = None
         self.rope: Optional[Rope] = None
         self.sparse_ratio: Optional[float] = None
@@ -177,14 +192,22 @@ class QwenDecoder:
         for li, layer in enumerate(self.layers):
             if li > 0:
                 h, residual = fe.fused_add_rms_norm(x, residual, layer.norm1, eps)
-            qkv = _linear(h, layer.w_qkv, layer.b_qkv)            # [B, (hq + 2 hk) hd]
             kmin = kmax = None
             if self.sparse_ratio is not None:
                 kmin, kmax = cache.page_bounds(li)
-            # RoPE, the K/V store at this step's slots (and the page bounds)
-            # and q folded to [B, hk, n_rep, hd], in one launch
-            fe.rope_write_decode(qkv, pos, self.rope.cos, self.rope.sin, slots, cache.k_pool[li],
-                                 cache.v_pool[li], hq, hk, q_out=q, kmin=kmin, kmax=kmax)
+            # the q/k/v projection, RoPE, the K/V store at this step's slots
+            # (and the page bounds) and q folded to [B, hk, n_rep, hd]: one
+            # launch at decode batch sizes (the projection's epilogue)
+            wq = layer.p_qkv if layer.p_qkv is not None else layer.w_qkv
+            if b <= HIP_GEMM_MAX_ROWS and dg.supports(h, wq):
+                dg.qkv_rope_write(h, wq, layer.b_qkv, pos, self.rope.cos, self.rope.sin,
+                                  slots, cache.k_pool[li], cache.v_pool[li], hq, hk, q_out=q,
+                                  kmin=kmin, kmax=kmax)
+            else:
+                qkv = F.linear(h, layer.w_qkv, layer.b_qkv)       # [B, (hq + 2 hk) hd]
+                fe.rope_write_decode(qkv, pos, self.rope.cos, self.rope.sin, slots,
+                                     cache.k_pool[li], cache.v_pool[li], hq, hk, q_out=q,
+                                     kmin=kmin, kmax=kmax)
             if self.sparse_ratio is None:
                 pdh.paged_decode_hip(q, cache.k_pool[li], cache.v_pool[li], tables, lens,
                                      max_seq_len=max_position + 1,
@@ -196,8 +219,9 @@ class QwenDecoder:
                                     kmax, ratio=self.sparse_ratio,
                                     recent=layer.attn.sparse_recent, max_seq_len=ctx,
                                     softmax_scale=self.scale, out=o)
-            x = _linear(o.view(b, hq * hd), layer.w_o)
+            x = _linear(o.view(b, hq * hd), layer.w_o, layer.p_o)
             h, residual = fe.fused_add_rms_norm(x, residual, layer.norm2, eps)
-            x = _linear(_gate_up_silu(h, layer.w_gate_up), layer.w_down)
+            x = _linear(_gate_up_silu(h, layer.w_gate_up, layer.p_gate_up), layer.w_down,
+                        layer.p_down)
         h, _ = fe.fused_add_rms_norm(x, residual, self.norm, eps)
-        return _linear(h, self.lm_head).view(b, 1, -1)
+        return _linear(h, self.lm_head, self.p_lm_head).view(b, 1, -1)

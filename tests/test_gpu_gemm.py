@@ -163,3 +163,93 @@ def test_split_product_in_a_graph_replays_exactly():
         torch.cuda.synchronize()
         assert torch.equal(out, want), i
         dg().linear(x, w)                          # eager work between replays
+
+
+@pytest.mark.parametrize("m", [1, 7, 16])
+@pytest.mark.parametrize("bounds", [False, True])
+def test_qkv_rope_write_is_the_gemm_then_rope_write_bit_for_bit(m, bounds):
+    """The fused q/k/v projection (Qwen2.5-1.5B: 12 / 2 heads of 128, K 1536,
+    bias) equals linear followed by rope_write_decode: q, the K/V pools and
+    the page bounds, bit for bit; slots -1 and past the pool store nothing."""
+    gen = torch.Generator(device="cuda").manual_seed(m * 3 + bounds)
+    hq, hk, d, k, nb, page = 12, 2, 128, 1536, 40, 16
+    n = (hq + 2 * hk) * d
+    x = torch.randn(m, k, device="cuda", generator=gen).half()
+    w = (torch.randn(n, k, device="cuda", generator=gen) * k**-0.5).half()
+    b = torch.randn(n, device="cuda", generator=gen).half()
+    ang = torch.rand(300, d // 2, device="cuda", generator=gen) * 6
+    cos = torch.cat([ang, ang], -1).cos().half()
+    sin = torch.cat([ang, ang], -1).sin().half()
+    pos = torch.randint(0, 400, (m,), device="cuda", generator=gen)        # some past the table
+    # distinct pages (a step writes each sequence into its own page)
+    pages = torch.randperm(nb, device="cuda", generator=gen)[:m]
+    slots = pages * page + torch.randint(0, page, (m,), device="cuda", generator=gen)
+    slots[0] = -1
+    if m > 2:
+        slots[2] = nb * page + 3                                            # past the pool
+        slots[1] = (slots[1] // page) * page                                # a page's first token
+    pools = [torch.randn(nb, page, hk, d, device="cuda", generator=gen).half() for _ in range(2)]
+    kmin = torch.randn(nb, hk, d, device="cuda", generator=gen).half()
+    kmax = kmin + 1
+    outs = []
+    for fused in (True, False):
+        K, V = pools[0].clone(), pools[1].clone()
+        mn, mx = kmin.clone(), kmax.clone()
+        kw = dict(kmin=mn, kmax=mx) if bounds else {}
+        if fused:
+            q = dg().qkv_rope_write(x, w, b, pos, cos, sin, slots, K, V, hq, hk, **kw)
+        else:
+            q = fe().rope_write_decode(dg().linear(x, w, b), pos, cos, sin, slots, K, V, hq, hk,
+                                       **kw)
+        outs.append((q, K, V, mn, mx))
+    torch.cuda.synchronize()
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("m", [1, 16, 40])
+@pytest.mark.parametrize("n,k", [(2048, 1536), (1536, 8960), (300, 64), (17920, 1536)])
+def test_packed_weight_gives_the_same_bits(m, n, k):
+    """A packed weight (every load 1 KiB contiguous; at <= 16 rows X through
+    LDS) gives the row-major path's outputs bit for bit, split K included."""
+    gen = torch.Generator(device="cuda").manual_seed(m + n)
+    x = torch.randn(m, k, device="cuda", generator=gen).half()
+    w = (torch.randn(n, k, device="cuda", generator=gen) * k**-0.5).half()
+    b = torch.randn(n, device="cuda", generator=gen).half()
+    pw = dg().PackedWeight(w, "plain")
+    y = dg().linear(x, pw, b)
+    torch.cuda.synchronize()
+    assert torch.equal(y, dg().linear(x, w, b))
+
+
+@pytest.mark.parametrize("m", [1, 7, 16])
+def test_packed_gate_up_and_qkv_give_the_same_bits(m):
+    gen = torch.Generator(device="cuda").manual_seed(m)
+    x = torch.randn(m, 1536, device="cuda", generator=gen).half()
+    wg = (torch.randn(2 * 8960, 1536, device="cuda", generator=gen) * 0.03).half()
+    assert torch.equal(dg().gate_up_silu(x, dg().PackedWeight(wg, "gate_up")),
+                       dg().gate_up_silu(x, wg))
+    hq, hk, d, nb, page = 12, 2, 128, 20, 16
+    n = (hq + 2 * hk) * d
+    w = (torch.randn(n, 1536, device="cuda", generator=gen) * 0.03).half()
+    b = torch.randn(n, device="cuda", generator=gen).half()
+    ang = torch.rand(64, d // 2, device="cuda", generator=gen) * 6
+    cos, sin = torch.cat([ang, ang], -1).cos().half(), torch.cat([ang, ang], -1).sin().half()
+    pos = torch.randint(0, 64, (m,), device="cuda", generator=gen)
+    slots = torch.randperm(nb, device="cuda", generator=gen)[:m] * page + 3
+    outs = []
+    for wk in (dg().PackedWeight(w, "qkv", d), w):
+        K = torch.zeros(nb, page, hk, d, device="cuda", dtype=torch.float16)
+        V = torch.zeros_like(K)
+        q = dg().qkv_rope_write(x, wk, b, pos, cos, sin, slots, K, V, hq, hk)
+        outs.append((q, K, V))
+    torch.cuda.synchronize()
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+
+
+def test_packed_weight_kind_is_checked():
+    w = torch.zeros(64, 64, device="cuda", dtype=torch.float16)
+    pw = dg().PackedWeight(w, "gate_up")
+    with pytest.raises(ValueError):
+        dg().linear(torch.zeros(2, 64, device="cuda", dtype=torch.float16), pw)
