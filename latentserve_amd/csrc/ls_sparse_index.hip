@@ -19,12 +19,14 @@
 //    page order, so the result is deterministic.  With a ratio the first n_b
 //    entries are the sequence's own budget (the rule the sparse decode kernel
 //    applies to the list), the rest of the k entries follow.  One 256-thread
-//    group a row, the row's keys in its registers (up to 32 a thread).
-//  * sparse_attention's selector is two launches, index then select.  A
-//    single launch in which the last index group of a row ran its selection
-//    was slower than the pair: its arrival count is a device-scope atomic
-//    issued while the other groups stream the page bounds, and such atomics
-//    take several microseconds to return under that traffic.
+//    group a row, the row's keys in its registers (up to 32 a thread); the
+//    select itself is in ls_select.h, shared with the sparse decode kernel,
+//    whose workgroups can run it on the scores in their prologue.
+//  * ls_sparse_index (index, then select) is two launches.  A single launch
+//    in which the last index group of a row ran its selection was slower
+//    than the pair: its arrival count is a device-scope atomic issued while
+//    the other groups stream the page bounds, and such atomics take several
+//    microseconds to return under that traffic.
 #include "ls_common.h"
 #include "ls_sparse.h"
 #include "ls_select.h"

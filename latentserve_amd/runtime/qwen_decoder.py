@@ -7,16 +7,15 @@ rebuilt: this is the minimum that gives the decode-attention path its real
 surroundings (28 layers, hidden 1536, 12 query / 2 KV heads, MLP 8960,
 vocab 151936, tied embeddings, RoPE theta 1e6, q/k/v biases) so a captured
 decode step can be timed on the reference's full-step configuration.  The
-projections run on the HIP weight-streaming GEMM up to 16 rows (hipBLASLt,
-through torch, above that, where it is faster), the MLP activation in the
-gate/up GEMM's epilogue and RoPE + the K/V store + the query fold in the
-q/k/v GEMM's; everything else is HIP as well: the embedding lookup inside
-the first norm, per layer the fused norms
-(residual add folded in), one launch for RoPE + the K/V store + the query
-fold (GQAAttention.forward's decode branch, model/attention/gqa.py:283-344:
-q [B, 12, 1, D] folded to [B, 2, 6, D], the new K/V written first), the
-paged decode attention writing straight into the output projection's
-input.
+projections run on the HIP weight-streaming GEMM with packed weights up to
+16 rows (hipBLASLt, through torch, above that, where it is faster); the
+MLP activation is in the gate/up GEMM's epilogue, and RoPE + the K/V store
++ the query fold (GQAAttention.forward's decode branch,
+model/attention/gqa.py:283-344: q [B, 12, 1, D] folded to [B, 2, 6, D],
+the new K/V written first) in the q/k/v GEMM's.  Everything else is HIP
+as well: the embedding lookup inside the first norm, per layer the fused
+norms (residual add folded in) and the paged decode attention, writing
+straight into the output projection's input.
 """
 
 from __future__ import annotations
