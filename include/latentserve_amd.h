@@ -329,7 +329,9 @@ int ls_decode_qkv_rope_write(const void* x, int64_t x_stride, const void* w, int
                              const int64_t* kv_strides, int num_blocks, int page, void* q_out,
                              const int64_t* q_strides, void* kmin, void* kmax,
                              const int64_t* bounds_strides, int batch, int hq, int hk,
-                             int head_dim, void* stream);
+                             int head_dim, const void* res, int64_t res_stride,
+                             const void* norm_w, float eps, void* res_out,
+                             int64_t res_out_stride, void* stream);
 
 /* y[r] = ls_rms_norm of table row ids[r] (int64, clamped into [0,
  * table_rows)), and rows_out[r] = that table row (NULL to skip): the token
@@ -368,6 +370,21 @@ size_t ls_gemm_packed_bytes(int N, int K, int kind, int head_dim);
 int ls_pack_gemm_weight(const void* w, int64_t w_stride, int N, int K, int kind, int head_dim,
                         void* packed, void* stream);
 
+/* The norm prologue of the three decode GEMMs below (ls_decode_gemm,
+ * ls_decode_gate_up_silu, ls_decode_qkv_rope_write): with norm_w non-NULL
+ * the product's left operand is not x but ls_rms_norm(x + res) (fp16 rows,
+ * weight norm_w [K], eps; the decoder layer's residual add and RMSNorm),
+ * and res_out receives x + res, as ls_rms_norm with a residual does; the
+ * sum of squares is taken in another order, so the normalised row may
+ * differ from ls_rms_norm's in the last fp16 bit.  Needs a packed weight,
+ * M <= 16 and a width at which K is not split over workgroups
+ * (ls_decode_gemm_workspace_bytes == 0); res, res_out (row strides
+ * res_stride, res_out_stride) and norm_w 16-byte aligned; res_out may not
+ * overlap x or res.  norm_w NULL: x is the operand and res, res_out are
+ * ignored.  Replaces the post_attention_layernorm / input_layernorm / final
+ * norm launch before each projection (kernels/fused_elementwise.py:194-205,
+ * model/latentserve_qwen.py:425-450). */
+
 /* y[M, N] = x[M, K] . w[N, K]^T (+ bias[N]) in fp16 with fp32 sums: the
  * projections of a decode step (torch Linear weight layout), M <= 64 rows.
  * Rows of x, w and y are strided (x_stride, w_stride, y_stride elements);
@@ -380,7 +397,9 @@ int ls_pack_gemm_weight(const void* w, int64_t w_stride, int N, int K, int kind,
  * which run as cuBLAS GEMMs. */
 int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
                    int w_packed, const void* bias, void* y, int64_t y_stride, int M, int N, int K,
-                   void* workspace, size_t workspace_bytes, void* stream);
+                   void* workspace, size_t workspace_bytes, const void* res, int64_t res_stride,
+                   const void* norm_w, float eps, void* res_out, int64_t res_out_stride,
+                   void* stream);
 
 /* Bytes of device `workspace` ls_decode_gemm needs for these sizes: fp32
  * partial sums and arrival counters when K is split over workgroups (narrow
@@ -402,7 +421,9 @@ size_t ls_decode_gemm_workspace_bytes(int M, int N, int K);
  * (kernels/fused_elementwise.py:222-233, model/fused.py). */
 int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
                            int w_packed, const void* bias, void* y, int64_t y_stride, int M,
-                           int inter, int K, void* stream);
+                           int inter, int K, const void* res, int64_t res_stride,
+                           const void* norm_w, float eps, void* res_out, int64_t res_out_stride,
+                           void* stream);
 
 /* Measurement only, no counterpart in the reference: the decode kernel's
  * page compute alone, from registers (groups x 8 waves, each applying one

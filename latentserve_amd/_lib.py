@@ -28,7 +28,7 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -81,18 +81,19 @@ _SIGNATURES = {
         _VP, _I64P, _I32, _I32, _I32, _I32, _VP],
     "ls_decode_qkv_rope_write": [
         _VP, _I64, _VP, _I64, _I32, _VP, _I32, _VP, _VP, _VP, _I64, _I32, _VP, _VP, _VP, _I64P, _I32,
-        _I32, _VP, _I64P, _VP, _VP, _I64P, _I32, _I32, _I32, _I32, _VP],
+        _I32, _VP, _I64P, _VP, _VP, _I64P, _I32, _I32, _I32, _I32,
+        _VP, _I64, _VP, _F32, _VP, _I64, _VP],
     "ls_embed_rms_norm": [
         _VP, _I64, _I64, _VP, _VP, _VP, _I64, _VP, _I64, _I32, _I32, _F32, _VP],
     "ls_argmax_workspace_bytes": [_I32, _I32],
     "ls_argmax_rows": [_VP, _I64, _VP, _I32, _I32, _VP, _SZ, _VP],
     "ls_decode_gemm": [_VP, _I64, _VP, _I64, _I32, _VP, _VP, _I64, _I32, _I32, _I32, _VP, _SZ,
-                       _VP],
+                       _VP, _I64, _VP, _F32, _VP, _I64, _VP],
     "ls_gemm_packed_bytes": [_I32, _I32, _I32, _I32],
     "ls_pack_gemm_weight": [_VP, _I64, _I32, _I32, _I32, _I32, _VP, _VP],
     "ls_decode_gemm_workspace_bytes": [_I32, _I32, _I32],
     "ls_decode_gate_up_silu": [_VP, _I64, _VP, _I64, _I32, _VP, _VP, _I64, _I32, _I32, _I32,
-                               _VP],
+                               _VP, _I64, _VP, _F32, _VP, _I64, _VP],
     "ls_compute_probe": [_I32, _I32, _I32, _F32, _VP, _VP],
     "ls_combine_splits": [
         _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],

@@ -184,13 +184,52 @@ bool weight_ok(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
     return w_packed || (w_stride % 8 == 0 && w_stride >= K);
 }
 
+
+// The norm prologue of a decode GEMM (norm_w non-null): x is replaced by
+// rms_norm(x + res) with weight norm_w, and x + res stored to res_out.
+// Needs a packed weight, M <= 16 and K not split over workgroups; res_out
+// is written while other workgroups read x and res, so it may alias
+// neither.
+int set_norm(ls::GemmParams& a, const void* res, int64_t res_stride, const void* norm_w,
+             float eps, void* res_out, int64_t res_out_stride, const char* what) {
+    if (!norm_w) return LS_OK;
+    if (!res || !res_out) return fail(LS_ERR_INVALID, "%s: the norm needs res and res_out", what);
+    if (!a.w_packed || a.M > 16)
+        return fail(LS_ERR_INVALID, "%s: the norm prologue needs a packed weight and M <= 16",
+                    what);
+    if (!aligned(res, 16) || !aligned(res_out, 16) || !aligned(norm_w, 16) ||
+        res_stride % 8 != 0 || res_out_stride % 8 != 0 ||
+        (a.M > 1 && (res_stride < a.K || res_out_stride < a.K)))
+        return fail(LS_ERR_INVALID,
+                    "%s: res, res_out and norm_w must be 16-byte aligned rows of K values", what);
+    const char* ro = (const char*)res_out;
+    const int64_t span = ((int64_t)(a.M - 1) * res_out_stride + a.K) * 2;
+    auto overlaps = [&](const void* p, int64_t stride) {
+        const char* q = (const char*)p;
+        const int64_t qspan = ((int64_t)(a.M - 1) * stride + a.K) * 2;
+        return q < ro + span && ro < q + qspan;
+    };
+    if (overlaps(res, res_stride) || overlaps(a.x, a.ldx))
+        return fail(LS_ERR_INVALID, "%s: res_out may not overlap x or res", what);
+    if (a.M > 0 && a.N > 0 && ls::decode_gemm_splits(a.M, a.N, a.K) != 1)
+        return fail(LS_ERR_INVALID, "%s: K %d is too long for the norm prologue", what, a.K);
+    a.norm = 1;
+    a.nres = res;
+    a.ldr = res_stride;
+    a.nw = norm_w;
+    a.nres_out = res_out;
+    a.ldro = res_out_stride;
+    a.eps = eps;
+    return LS_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 12; }
+int ls_abi_version(void) { return 13; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -860,7 +899,9 @@ int ls_decode_qkv_rope_write(const void* x, int64_t x_stride, const void* w, int
                              const int64_t* kv_strides, int num_blocks, int page, void* q_out,
                              const int64_t* q_strides, void* kmin, void* kmax,
                              const int64_t* bounds_strides, int batch, int hq, int hk,
-                             int head_dim, void* stream) {
+                             int head_dim, const void* res, int64_t res_stride,
+                             const void* norm_w, float eps, void* res_out,
+                             int64_t res_out_stride, void* stream) {
     ls::GemmParams a;
     const int rc = make_rope_params(a.rope, x, 0, positions, cos, sin, table_stride, table_rows,
                                     slots, k_pool, v_pool, kv_strides, num_blocks, page, q_out,
@@ -897,6 +938,9 @@ int ls_decode_qkv_rope_write(const void* x, int64_t x_stride, const void* w, int
     a.counters = nullptr;
     a.splits = 1;
     a.epi = ls::GEMM_ROPE;
+    if (int nrc = set_norm(a, res, res_stride, norm_w, eps, res_out, res_out_stride,
+                           "ls_decode_qkv_rope_write"))
+        return nrc;
     return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_qkv_rope_write");
 }
 
@@ -907,7 +951,9 @@ size_t ls_decode_gemm_workspace_bytes(int M, int N, int K) {
 
 int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
                    int w_packed, const void* bias, void* y, int64_t y_stride, int M, int N, int K,
-                   void* workspace, size_t workspace_bytes, void* stream) {
+                   void* workspace, size_t workspace_bytes, const void* res, int64_t res_stride,
+                   const void* norm_w, float eps, void* res_out, int64_t res_out_stride,
+                   void* stream) {
     if (!x || !w || !y) return fail(LS_ERR_INVALID, "null pointer argument");
     if (M < 0 || M > ls::GEMM_MAX_M || N < 0 || K < 32 || K % 32 != 0)
         return fail(LS_ERR_INVALID,
@@ -946,12 +992,17 @@ int ls_decode_gemm(const void* x, int64_t x_stride, const void* w, int64_t w_str
         a.counters = (unsigned*)workspace;
         a.part = (float*)((char*)workspace + ls::GEMM_PART_OFFSET);
     }
+    if (int nrc = set_norm(a, res, res_stride, norm_w, eps, res_out, res_out_stride,
+                           "ls_decode_gemm"))
+        return nrc;
     return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_gemm");
 }
 
 int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64_t w_stride,
                            int w_packed, const void* bias, void* y, int64_t y_stride, int M,
-                           int inter, int K, void* stream) {
+                           int inter, int K, const void* res, int64_t res_stride,
+                           const void* norm_w, float eps, void* res_out, int64_t res_out_stride,
+                           void* stream) {
     if (!x || !w || !y) return fail(LS_ERR_INVALID, "null pointer argument");
     if (M < 0 || M > ls::GEMM_MAX_M || inter < 0 || inter > (1 << 29) || K < 32 || K % 32 != 0)
         return fail(LS_ERR_INVALID,
@@ -983,6 +1034,9 @@ int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64
     a.counters = nullptr;
     a.splits = 1;
     a.epi = ls::GEMM_GLU;
+    if (int nrc = set_norm(a, res, res_stride, norm_w, eps, res_out, res_out_stride,
+                           "ls_decode_gate_up_silu"))
+        return nrc;
     return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_gate_up_silu");
 }
 

@@ -27,6 +27,17 @@ struct GemmParams {
                          // [gate; up], GEMM_ROPE: the fused q/k/v projection's outputs
                          // rotated and stored as `rope` describes (y unused)
     RopeWriteParams rope;
+    // norm != 0: the X operand is rms_norm(x + nres) (the decode layer's
+    // residual add and RMSNorm, weight nw, eps), computed in the prologue;
+    // workgroup 0 stores x + nres to nres_out.  One column block, K not
+    // split over workgroups.
+    int norm = 0;
+    const void* nres = nullptr;
+    int64_t ldr = 0;
+    const void* nw = nullptr;
+    void* nres_out = nullptr;
+    int64_t ldro = 0;
+    float eps = 0.f;
 };
 
 enum GemmEpilogue { GEMM_PLAIN = 0, GEMM_GLU = 1, GEMM_ROPE = 2 };

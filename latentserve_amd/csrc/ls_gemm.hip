@@ -196,9 +196,45 @@ __device__ __forceinline__ void rope_store(const RopeWriteParams& a, int m, int 
 // one row each) and read from there in MFMA order; the same LDS then holds
 // the wave's partial tiles for the group's sum.  (X loaded straight to
 // registers reads 64 bytes of each of 16 rows per instruction.)
-template <int SPW, int TPW, int MB, int EPI, bool PW, bool LX>
+// One step of a reduce-scatter over the lanes: lanes with `BIT` clear keep
+// values 0 .. HALF - 1 and send the upper HALF, lanes with it set the
+// reverse; each kept value adds the partner's.  (Selecting by value keeps
+// the array in registers; selecting an index would turn into a search.)
+// h = fp16(w * fp16(s * inv)) on 8 channels: the fp32 scale rounded to
+// fp16, then the weight product in packed fp16 (exact product, one rounding)
+__device__ __forceinline__ u4 norm_row(u4 sv, u4 wv, float inv) {
+    // (bit casts take named scalars: this compiler casts an element of a
+    // vector lvalue from the vector's first element)
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    uint32_t hw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const h2 s2 = __builtin_bit_cast(h2, sw[e]);
+        const h2 n2 = {(half_t)((float)s2.x * inv), (half_t)((float)s2.y * inv)};
+        hw[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ww[e]) * n2);
+    }
+    return (u4){hw[0], hw[1], hw[2], hw[3]};
+}
+
+template <int HALF, int BIT>
+__device__ __forceinline__ void reduce_step(float* v, int lane) {
+    const uint32_t hi = (lane & BIT) ? ~0u : 0u;
+#pragma unroll
+    for (int j = 0; j < HALF; ++j) {
+        const uint32_t a = __builtin_bit_cast(uint32_t, v[j]);
+        const uint32_t b = __builtin_bit_cast(uint32_t, v[j + HALF]);
+        const float send = __builtin_bit_cast(float, (a & hi) | (b & ~hi));
+        const float keep = __builtin_bit_cast(float, (b & hi) | (a & ~hi));
+        v[j] = keep + __shfl_xor(send, BIT);
+    }
+}
+
+template <int SPW, int TPW, int MB, int EPI, bool PW, bool LX, bool NRM = false>
 __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
     static_assert(!LX || (MB == 1 && SPW == 16), "LDS X: one column block, 16-step chunks");
+    static_assert(!NRM || LX, "the norm prologue works on the LDS rows");
+    __shared__ float nrm_part[NRM ? 4 : 1][16];       // [wave][row] sums of squares
     extern __shared__ f4 red[];                       // [waves][TPW][MB][WAVE] (LX: per wave)
     const int nw = blockDim.x / WAVE;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
@@ -259,15 +295,103 @@ __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
             for (int mb = 0; mb < MB; ++mb) xb[i][mb] = *(const u4*)(xp[mb] + 32 * st);
         }
     }
+    // norm prologue: this lane's residual channels of every row, and the
+    // norm weight of its channels (requested before the weight loads)
+    u4 rv[NRM ? 16 : 1];
+    u4 nwv = {0u, 0u, 0u, 0u};
+    const int ncol = 32 * s0 + 8 * lane < a.K - 8 ? 32 * s0 + 8 * lane : a.K - 8;
+    if constexpr (NRM) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int m = q < a.M ? q : a.M - 1;
+            rv[q] = *(const u4*)((const half_t*)a.nres + (int64_t)m * a.ldr + ncol);
+        }
+        nwv = *(const u4*)((const half_t*)a.nw + ncol);
+    }
     load_w(0, 0);
-    if (TPW > 1) load_w(1, 1);
+    // with the norm prologue the second tile's weights are requested after
+    // it, so the residual rows and those weights are not in registers at once
+    if (TPW > 1 && !NRM) load_w(1, 1);
     if constexpr (LX) {
         // the X rows were requested before every weight load: once no more
         // than the weight loads are outstanding, they are in LDS
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_wait(SPW * (TPW > 1 ? 2 : 1)));
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(SPW * (TPW > 1 && !NRM ? 2 : 1)));
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (NRM) {
+        // Every workgroup normalises the rows itself (they are 16 x K), so
+        // this is written for few instructions: packed fp16 adds and
+        // multiplies, which round as the fp32 operation rounded to fp16 does
+        // (the fp32 sum or product of two fp16 values is exact, or rounds
+        // innocuously), and one butterfly reduce-scatter for the 16 rows'
+        // sums of squares.
+        //
+        // s = res + x (fp16) on the lane's 8 channels of each row, written
+        // over x in LDS; channels past the wave's chunk belong to the next
+        // wave and are not counted.
+        const bool mine = 8 * lane < 32 * ns;
+        float ss[16];
+        u4 sv[16];
+        // all 16 reads first, then the sums, then the writes: one LDS round
+        // trip for the rows rather than one a row
+#pragma unroll
+        for (int q = 0; q < 16; ++q) sv[q] = *(const u4*)(xl + q * XROW_BYTES + lane * 16);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const uint32_t xw[4] = {sv[q].x, sv[q].y, sv[q].z, sv[q].w};
+            const uint32_t rw[4] = {rv[q].x, rv[q].y, rv[q].z, rv[q].w};
+            uint32_t sw[4];
+            float acc = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const h2 t = __builtin_bit_cast(h2, rw[e]) + __builtin_bit_cast(h2, xw[e]);
+                acc = __builtin_amdgcn_fdot2(t, t, acc, false);
+                sw[e] = __builtin_bit_cast(uint32_t, t);
+            }
+            sv[q] = (u4){sw[0], sw[1], sw[2], sw[3]};
+            ss[q] = mine ? acc : 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < 16; ++q) *(u4*)(xl + q * XROW_BYTES + lane * 16) = sv[q];
+        // workgroup 0 stores the new residual (its waves cover the row)
+        if (blockIdx.x == 0 && mine) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q)
+                if (q < a.M) *(u4*)((half_t*)a.nres_out + (int64_t)q * a.ldro + ncol) = sv[q];
+        }
+        // reduce-scatter over the lanes: after the xor-32/16/8/4 steps lane l
+        // holds row (l >> 2) summed over the 16 lanes sharing its low 2 bits
+        reduce_step<8, 32>(ss, lane);
+        reduce_step<4, 16>(ss, lane);
+        reduce_step<2, 8>(ss, lane);
+        reduce_step<1, 4>(ss, lane);
+        float tot = ss[0];
+        tot += __shfl_xor(tot, 2);
+        tot += __shfl_xor(tot, 1);
+        if ((lane & 3) == 0) nrm_part[wv][lane >> 2] = tot;
+        __syncthreads();
+        if (TPW > 1) load_w(1, 1);
+        // lane q < 16: 1 / rms of row q over the group's waves (in wave order)
+        float inv;
+        {
+            const int q = lane & 15;
+            float t = 0.f;
+            for (int p = 0; p < nw; ++p) t += nrm_part[p][q];
+            inv = 1.f / sqrtf(t / (float)a.K + a.eps);
+        }
+        // h = fp16(w * fp16(s * inv)) in place, the rounding of Qwen2RMSNorm
+        // in fp16 (applied here once rather than per weight tile as the
+        // product reads the rows: that costs more where tiles are many)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            char* row = xl + q * XROW_BYTES + lane * 16;
+            const float iq = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv), q));
+            *(u4*)row = norm_row(*(const u4*)row, nwv, iq);
+        }
+        asm volatile("" ::: "memory");
     }
     f4 acc[TPW][MB];
 #pragma unroll
@@ -499,8 +623,12 @@ void launch_kernel(const GemmParams& p, const GemmShape& sh, hipStream_t stream)
     const dim3 grid(sh.units, p.splits), block(WAVE * sh.group_waves);
     if (p.w_packed && MB == 1) {
         const size_t lds = (size_t)sh.group_waves * XREG_BYTES;
-        hipLaunchKernelGGL((decode_gemm_kernel<spw_for(MB), TPW, MB, EPI, true, MB == 1>), grid,
-                           block, lds, stream, p);
+        if (p.norm)
+            hipLaunchKernelGGL((decode_gemm_kernel<spw_for(MB), TPW, MB, EPI, true, MB == 1, MB == 1>),
+                               grid, block, lds, stream, p);
+        else
+            hipLaunchKernelGGL((decode_gemm_kernel<spw_for(MB), TPW, MB, EPI, true, MB == 1>),
+                               grid, block, lds, stream, p);
         return;
     }
     const size_t lds =
@@ -586,6 +714,9 @@ hipError_t launch_decode_gemm(const GemmParams& p, hipStream_t stream) {
     if (p.M == 0 || p.N == 0) return hipSuccess;
     const GemmShape sh = gemm_shape(p.M, p.N, p.K);
     if (sh.splits != p.splits || sh.group_waves > MAX_GROUP_WAVES) return hipErrorInvalidValue;
+    // the norm prologue: the LDS X path (packed weight, one column block),
+    // a group covering the whole row
+    if (p.norm && (!p.w_packed || sh.mb != 1 || p.splits != 1)) return hipErrorInvalidValue;
     if (p.epi == GEMM_GLU) {
         if (p.splits != 1 || p.N % 2 != 0) return hipErrorInvalidValue;
         launch_any<GEMM_GLU>(p, sh, stream);

@@ -100,6 +100,30 @@ def _weight_args(weight, kind: str):
     return weight.data_ptr(), weight.stride(0), 0, tuple(weight.shape)
 
 
+def _norm_args(x2: torch.Tensor, m: int, k: int, residual, norm_weight, eps, res_out):
+    """ctypes arguments of the norm prologue, and the res_out it writes.
+
+    norm_weight None: no prologue (x is the operand).  Otherwise the operand
+    is rms_norm(x + residual) with norm_weight and eps, and x + residual goes
+    to res_out (allocated when None; it may not overlap x or residual)."""
+    if norm_weight is None:
+        return (None, 0, None, 0.0, None, 0), None
+    if residual is None:
+        raise ValueError("the norm prologue needs the residual")
+    r2 = residual.reshape(-1, k)
+    for name, t in (("residual", r2), ("norm_weight", norm_weight)):
+        if not t.is_cuda or t.dtype != torch.float16:
+            raise ValueError(f"{name} must be fp16 on the GPU")
+    if r2.shape[0] != m or norm_weight.shape != (k,) or not norm_weight.is_contiguous():
+        raise ValueError(f"residual must be [{m}, {k}] and norm_weight contiguous [{k}]")
+    if r2.stride(-1) != 1 or (m > 1 and r2.stride(0) % 8) or r2.data_ptr() % 16:
+        r2 = r2.contiguous()
+    ro = torch.empty((m, k), dtype=x2.dtype, device=x2.device) if res_out is None \
+        else res_out.view(m, k)
+    return (r2.data_ptr(), r2.stride(0) if m > 1 else k, norm_weight.data_ptr(), float(eps),
+            ro.data_ptr(), ro.stride(0) if m > 1 else k), ro
+
+
 def supports(x: torch.Tensor, weight) -> bool:
     """Whether ``linear`` takes these operands without a copy."""
     if isinstance(weight, PackedWeight):
@@ -114,8 +138,14 @@ def supports(x: torch.Tensor, weight) -> bool:
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
-           out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y = x . weight^T (+ bias) for x [..., K] fp16 with at most 64 rows."""
+           out: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+           norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+           res_out: Optional[torch.Tensor] = None):
+    """y = x . weight^T (+ bias) for x [..., K] fp16 with at most 64 rows.
+
+    With norm_weight (a packed weight, at most 16 rows): y = rms_norm(x +
+    residual) . weight^T (+ bias) in one launch, returning (y, x +
+    residual)."""
     for name, t in (("x", x), ("weight", weight)):
         if not t.device.type == "cuda":
             raise ValueError(f"{name} must be on a GPU (the HIP kernels have no CPU path)")
@@ -135,22 +165,29 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
                              or not bias.is_contiguous()):
         raise ValueError(f"bias must be contiguous fp16 [{n}]")
     y = torch.empty((m, n), dtype=x.dtype, device=x.device) if out is None else out.view(m, n)
+    nargs, ro = _norm_args(x2, m, k, residual, norm_weight, eps, res_out)
     if m == 0 or n == 0:
-        return y.view(*x.shape[:-1], n)
+        return y.view(*x.shape[:-1], n) if ro is None else (y.view(*x.shape[:-1], n), ro)
     need = workspace_bytes(m, n, k)
     ws = _workspace(x.device, need) if need else None
     rc = _lib.lib().ls_decode_gemm(
         x2.data_ptr(), x2.stride(0) if m > 1 else k, wptr, wstride, packed,
         None if bias is None else bias.data_ptr(), y.data_ptr(),
         y.stride(0) if m > 1 else n, m, n, k, None if ws is None else ws.data_ptr(), need,
-        torch.cuda.current_stream(x.device).cuda_stream)
+        *nargs, torch.cuda.current_stream(x.device).cuda_stream)
     _lib.check(rc, "ls_decode_gemm")
-    return y.view(*x.shape[:-1], n)
+    y = y.view(*x.shape[:-1], n)
+    return y if ro is None else (y, ro)
 
 
 def gate_up_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 out: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+                 norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                 res_out: Optional[torch.Tensor] = None):
     """silu(x . Wg^T) * (x . Wu^T) for weight = [Wg; Wu] [2I, K]: [..., I].
+
+    With norm_weight, x is first replaced by rms_norm(x + residual) in the
+    same launch, and (y, x + residual) is returned (as linear).
 
     One launch where the product needs no split of K over workgroups;
     otherwise the GEMM and then the activation kernel (still HIP, same
@@ -173,7 +210,7 @@ def gate_up_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Ten
     if m > MAX_ROWS:
         raise ValueError(f"at most {MAX_ROWS} rows a call, got {m}")
     if m and inter and workspace_bytes(m, n2, k):
-        if packed:
+        if packed or norm_weight is not None:
             raise ValueError("this K splits over workgroups: pass the row-major weight")
         return fe.silu_and_mul(linear(x, weight, bias), out=out)
     if bias is not None and (bias.shape != (n2,) or bias.dtype != torch.float16
@@ -181,15 +218,18 @@ def gate_up_silu(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Ten
         raise ValueError(f"bias must be contiguous fp16 [{n2}]")
     y = torch.empty((m, inter), dtype=x.dtype, device=x.device) if out is None \
         else out.view(m, inter)
+    nargs, ro = _norm_args(x2, m, k, residual, norm_weight, eps, res_out)
     if m == 0 or inter == 0:
-        return y.view(*x.shape[:-1], inter)
+        y = y.view(*x.shape[:-1], inter)
+        return y if ro is None else (y, ro)
     rc = _lib.lib().ls_decode_gate_up_silu(
         x2.data_ptr(), x2.stride(0) if m > 1 else k, wptr, wstride, packed,
         None if bias is None else bias.data_ptr(), y.data_ptr(),
-        y.stride(0) if m > 1 else inter, m, inter, k,
+        y.stride(0) if m > 1 else inter, m, inter, k, *nargs,
         torch.cuda.current_stream(x.device).cuda_stream)
     _lib.check(rc, "ls_decode_gate_up_silu")
-    return y.view(*x.shape[:-1], inter)
+    y = y.view(*x.shape[:-1], inter)
+    return y if ro is None else (y, ro)
 
 
 def qkv_rope_write(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
@@ -197,8 +237,13 @@ def qkv_rope_write(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
                    slots: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, hq: int,
                    hk: int, q_out: Optional[torch.Tensor] = None,
                    kmin: Optional[torch.Tensor] = None,
-                   kmax: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   kmax: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+                   norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                   res_out: Optional[torch.Tensor] = None):
     """rope_write_decode(linear(x, weight, bias), ...) in one launch.
+
+    With norm_weight, x is first replaced by rms_norm(x + residual) in the
+    same launch, and (q, x + residual) is returned.
 
     x [B, K] (or [B, 1, K]) fp16; weight [(hq + 2 hk) * D, K]; the rest as
     fused_elementwise.rope_write_decode.  Returns q folded to [B, hk, hq //
@@ -219,7 +264,7 @@ def qkv_rope_write(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
     two = (n != (hq + 2 * hk) * d or d % 16 or b > MAX_ROWS or not supports(x2, weight)
            or (b and workspace_bytes(b, n, k)))
     if two:
-        if packed:
+        if packed or norm_weight is not None:
             raise ValueError("this shape takes two launches: pass the row-major weight")
         return fe.rope_write_decode(linear(x2, weight, bias), positions, cos, sin, slots, k_pool,
                                     v_pool, hq, hk, q_out=q_out, kmin=kmin, kmax=kmax)
@@ -230,9 +275,10 @@ def qkv_rope_write(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.T
         raise ValueError(f"bias must be contiguous fp16 [{n}]")
     args = fe.rope_write_args(positions, cos, sin, slots, k_pool, v_pool, hq, hk, b, d, q_out,
                               kmin, kmax)
+    nargs, ro = _norm_args(x2, b, k, residual, norm_weight, eps, res_out)
     rc = _lib.lib().ls_decode_qkv_rope_write(
         x2.data_ptr(), x2.stride(0) if b > 1 else k, wptr, wstride, packed,
-        None if bias is None else bias.data_ptr(), k, *args["pre"], b, hq, hk, d,
+        None if bias is None else bias.data_ptr(), k, *args["pre"], b, hq, hk, d, *nargs,
         torch.cuda.current_stream(x.device).cuda_stream)
     _lib.check(rc, "ls_decode_qkv_rope_write")
-    return args["q_out"]
+    return args["q_out"] if ro is None else (args["q_out"], ro)

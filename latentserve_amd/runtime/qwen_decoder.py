@@ -53,6 +53,15 @@ def _linear(x: torch.Tensor, w: torch.Tensor, pw=None,
     return F.linear(x, w, b)
 
 
+def _norm_folds(x: torch.Tensor, pw) -> bool:
+    """Whether the RMSNorm before the projection with packed weight pw can
+    run in its prologue: at most 16 rows and K not split over workgroups."""
+    if pw is None or x.shape[0] > 16 or not dg.supports(x, pw):
+        return False
+    n = pw.shape[0]
+    return dg.workspace_bytes(x.shape[0], n, pw.shape[1]) == 0
+
+
 def _gate_up_silu(x: torch.Tensor, w: torch.Tensor, pw=None) -> torch.Tensor:
     wk = pw if pw is not None else w
     if x.shape[0] <= HIP_GEMM_MAX_ROWS and dg.supports(x, wk):
@@ -189,7 +198,11 @@ class QwenDecoder:
                                         eps)
         x = None
         for li, layer in enumerate(self.layers):
-            if li > 0:
+            # with packed weights at decode batch sizes the norm before a
+            # projection runs in that projection's prologue (x + residual is
+            # written to a new buffer: it may not alias its inputs)
+            fold1 = li > 0 and _norm_folds(x, layer.p_qkv)
+            if li > 0 and not fold1:
                 h, residual = fe.fused_add_rms_norm(x, residual, layer.norm1, eps)
             kmin = kmax = None
             if self.sparse_ratio is not None:
@@ -198,7 +211,12 @@ class QwenDecoder:
             # (and the page bounds) and q folded to [B, hk, n_rep, hd]: one
             # launch at decode batch sizes (the projection's epilogue)
             wq = layer.p_qkv if layer.p_qkv is not None else layer.w_qkv
-            if b <= HIP_GEMM_MAX_ROWS and dg.supports(h, wq):
+            if fold1:
+                _, residual = dg.qkv_rope_write(
+                    x, wq, layer.b_qkv, pos, self.rope.cos, self.rope.sin, slots,
+                    cache.k_pool[li], cache.v_pool[li], hq, hk, q_out=q, kmin=kmin, kmax=kmax,
+                    residual=residual, norm_weight=layer.norm1, eps=eps)
+            elif b <= HIP_GEMM_MAX_ROWS and dg.supports(h, wq):
                 dg.qkv_rope_write(h, wq, layer.b_qkv, pos, self.rope.cos, self.rope.sin,
                                   slots, cache.k_pool[li], cache.v_pool[li], hq, hk, q_out=q,
                                   kmin=kmin, kmax=kmax)
@@ -219,8 +237,14 @@ class QwenDecoder:
                                     recent=layer.attn.sparse_recent, max_seq_len=ctx,
                                     softmax_scale=self.scale, out=o)
             x = _linear(o.view(b, hq * hd), layer.w_o, layer.p_o)
+            # (the gate/up projection keeps its norm launch: over its 1120
+            # workgroups the prologue costs more than the launch it saves)
             h, residual = fe.fused_add_rms_norm(x, residual, layer.norm2, eps)
             x = _linear(_gate_up_silu(h, layer.w_gate_up, layer.p_gate_up), layer.w_down,
                         layer.p_down)
+        if _norm_folds(x, self.p_lm_head):
+            logits, _ = dg.linear(x, self.p_lm_head, residual=residual, norm_weight=self.norm,
+                                  eps=eps)
+            return logits.view(b, 1, -1)
         h, _ = fe.fused_add_rms_norm(x, residual, self.norm, eps)
         return _linear(h, self.lm_head, self.p_lm_head).view(b, 1, -1)

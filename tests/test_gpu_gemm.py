@@ -253,3 +253,111 @@ def test_packed_weight_kind_is_checked():
     pw = dg().PackedWeight(w, "gate_up")
     with pytest.raises(ValueError):
         dg().linear(torch.zeros(2, 64, device="cuda", dtype=torch.float16), pw)
+
+
+def _normed_operand_bound(h_ref, w):
+    """Per-output bound for a product whose operand rows may differ from
+    h_ref by one fp16 step per element (the prologue sums the squares in
+    another order than the norm kernel, which can move the scale's last
+    bit): sum_k |h_k| |w_nk| 2^-10, plus two fp16 roundings of y."""
+    return (h_ref.float().abs() @ w.float().abs().t()) * 2.0**-10
+
+
+@pytest.mark.parametrize("m", [1, 7, 16])
+@pytest.mark.parametrize("n,k", [(1536, 1536), (300, 64), (2048, 1120), (151936, 1536)])
+def test_norm_prologue_matches_the_norm_then_the_gemm(m, n, k):
+    """linear(x, residual=, norm_weight=) equals fused_add_rms_norm followed by
+    the GEMM: x + residual bit for bit, y within what one fp16 step of the
+    normalised operand moves it (and bit-equal in most places)."""
+    gen = torch.Generator(device="cuda").manual_seed(m * 5 + n + k)
+    x = torch.randn(m, k, device="cuda", generator=gen).half()
+    res = (torch.randn(m, k, device="cuda", generator=gen) * 4).half()
+    nw = (torch.rand(k, device="cuda", generator=gen) + 0.5).half()
+    w = (torch.randn(n, k, device="cuda", generator=gen) * k**-0.5).half()
+    b = torch.randn(n, device="cuda", generator=gen).half()
+    pw = dg().PackedWeight(w, "plain")
+    if dg().workspace_bytes(m, n, k):
+        pytest.skip("splits K")
+    y, ro = dg().linear(x, pw, b, residual=res, norm_weight=nw, eps=1e-6)
+    h_ref, r_ref = fe().fused_add_rms_norm(x, res, nw, 1e-6)
+    y_ref = dg().linear(h_ref, pw, b)
+    torch.cuda.synchronize()
+    assert torch.equal(ro, r_ref)
+    err = (y.float() - y_ref.float()).abs()
+    tol = _normed_operand_bound(h_ref, w) + y_ref.float().abs() * 2.0**-10 + 1e-3
+    assert (err <= tol).all(), (err / tol).max().item()
+    assert (y == y_ref).float().mean().item() > 0.5
+    # against fp32 end to end: a dropped weight or residual would fail here
+    s = res.float() + x.float()
+    want = (s * torch.rsqrt(s.pow(2).mean(-1, keepdim=True) + 1e-6)) * nw.float() @ w.float().t()
+    want = want + b.float()
+    assert ((y.float() - want).abs() <= want.abs() * 2.0**-8 + 2e-2).all()
+
+
+@pytest.mark.parametrize("m", [1, 16])
+def test_norm_prologue_gate_up_and_qkv(m):
+    gen = torch.Generator(device="cuda").manual_seed(100 + m)
+    k = 1536
+    x = torch.randn(m, k, device="cuda", generator=gen).half()
+    res = (torch.randn(m, k, device="cuda", generator=gen) * 4).half()
+    nw = (torch.rand(k, device="cuda", generator=gen) + 0.5).half()
+    h_ref, r_ref = fe().fused_add_rms_norm(x, res, nw, 1e-6)
+    wg = (torch.randn(2 * 8960, k, device="cuda", generator=gen) * 0.03).half()
+    pg = dg().PackedWeight(wg, "gate_up")
+    g, ro = dg().gate_up_silu(x, pg, residual=res, norm_weight=nw, eps=1e-6)
+    g_ref = dg().gate_up_silu(h_ref, pg)
+    torch.cuda.synchronize()
+    assert torch.equal(ro, r_ref)
+    assert (g == g_ref).float().mean().item() > 0.5
+    # silu(a) * b moves by at most ~1.1 (|b| da + |silu(a)| db) for the bound of each
+    gu = h_ref.float() @ wg.float().t()
+    bnd = _normed_operand_bound(h_ref, wg)
+    a, bb = gu[:, :8960], gu[:, 8960:]
+    tol = 1.2 * (bb.abs() * bnd[:, :8960] + torch.nn.functional.silu(a).abs() * bnd[:, 8960:])
+    tol = tol + g_ref.float().abs() * 2.0**-9 + 2e-3
+    assert ((g.float() - g_ref.float()).abs() <= tol).all()
+
+    hq, hk, d, nb, page = 12, 2, 128, 20, 16
+    n = (hq + 2 * hk) * d
+    w = (torch.randn(n, k, device="cuda", generator=gen) * 0.03).half()
+    b = torch.randn(n, device="cuda", generator=gen).half()
+    ang = torch.rand(64, d // 2, device="cuda", generator=gen) * 6
+    cos, sin = torch.cat([ang, ang], -1).cos().half(), torch.cat([ang, ang], -1).sin().half()
+    pos = torch.randint(0, 64, (m,), device="cuda", generator=gen)
+    slots = torch.randperm(nb, device="cuda", generator=gen)[:m] * page + 3
+    pq = dg().PackedWeight(w, "qkv", d)
+    outs = []
+    for fused in (True, False):
+        K = torch.zeros(nb, page, hk, d, device="cuda", dtype=torch.float16)
+        V = torch.zeros_like(K)
+        if fused:
+            q, ro = dg().qkv_rope_write(x, pq, b, pos, cos, sin, slots, K, V, hq, hk,
+                                        residual=res, norm_weight=nw, eps=1e-6)
+            assert torch.equal(ro, r_ref)
+        else:
+            q = dg().qkv_rope_write(h_ref, pq, b, pos, cos, sin, slots, K, V, hq, hk)
+        outs.append((q, K, V))
+    torch.cuda.synchronize()
+    # RoPE mixes two channels with |cos|, |sin| <= 1: twice the product bound
+    qkv_bnd = _normed_operand_bound(h_ref, w)
+    for a_, c_ in zip(*outs):
+        err = (a_.float() - c_.float()).abs()
+        assert err.max().item() <= 2 * qkv_bnd.max().item() + 2.0**-8 * c_.float().abs().max()
+
+
+def test_norm_prologue_rejections():
+    k = 64
+    x = torch.randn(4, k, device="cuda").half()
+    res = torch.randn(4, k, device="cuda").half()
+    nw = torch.ones(k, device="cuda", dtype=torch.float16)
+    w = torch.randn(32, k, device="cuda").half()
+    pw = dg().PackedWeight(w, "plain")
+    with pytest.raises(ValueError):                # res_out aliasing the residual
+        dg().linear(x, pw, residual=res, norm_weight=nw, res_out=res)
+    with pytest.raises(ValueError):                # res_out aliasing x
+        dg().linear(x, pw, residual=res, norm_weight=nw, res_out=x)
+    with pytest.raises(ValueError):                # row-major weight
+        dg().linear(x, w, residual=res, norm_weight=nw)
+    with pytest.raises(ValueError):                # more than 16 rows
+        x17 = torch.randn(17, k, device="cuda").half()
+        dg().linear(x17, pw, residual=x17.clone(), norm_weight=nw)
