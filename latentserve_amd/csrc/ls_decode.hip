@@ -852,15 +852,24 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     };
     auto walk = [&](auto resolve, auto first) {
         if constexpr (HAS_RES) {
-            static_assert(HG == 1, "INT8 groups serve one head");
-            if (ends_seq && res_ok && wv == NWT - 1) {
+            // the last wave computes head h0's last page, the one before it
+            // head h0 + 1's
+            const int hr = NWT - 1 - wv;
+            if (ends_seq && res_ok && hr < HG) {
                 const int lp = num_pages - 1;
                 const int blk = a.block_tables[(int64_t)b * a.sbt_b + lp];
                 const bool okb = blk >= 0 && blk < a.num_blocks;
                 PageBuf rb;
-                load_page<KIND, ASYM, true>(a, rb, okb ? blk : 0, lp, num_pages, res_row, h0, g, c);
-                compute_page<KIND, ASYM>(rb, st[0], qh[0], okb ? lp : -1, okb ? len : 0,
-                                         scale_log2, g, sm.kscale[wv]);
+                load_page<KIND, ASYM, true>(a, rb, okb ? blk : 0, lp, num_pages, res_row, h0 + hr,
+                                            g, c);
+                auto res_into = [&](int hh) {
+                    compute_page<KIND, ASYM>(rb, st[hh], qh[hh], okb ? lp : -1, okb ? len : 0,
+                                             scale_log2, g, sm.kscale[wv]);
+                };
+                if (HG == 1 || hr == 0)
+                    res_into(0);
+                else
+                    res_into(HG - 1);
             }
         }
         auto issue_with = [&](auto res, int slot, int it) {
@@ -1092,9 +1101,10 @@ constexpr int NWAVES = 4;
 template <int KIND, bool ASYM, bool HAS_RES, int SPARSE, int ABL = 0>
 static hipError_t launch_t(const DecodeParams& a, hipStream_t stream) {
     // Heads in pairs when the head count allows: both halves of every token
-    // row are then read together (the fp16 walk; INT8 keeps one head per
-    // group for its larger register footprint).
-    if constexpr (KIND == KV_FP16) {
+    // row are then read together.
+    // INT8 too (c4 37.0 -> 35.8 us), except asymmetric pools, whose zero
+    // points would push the two-head state past the register file (spills)
+    if constexpr (KIND == KV_FP16 || !ASYM) {
         if (a.H % 2 == 0) {
         dim3 grid(a.num_splits * (a.H / 2), a.B);
         hipLaunchKernelGGL((paged_decode_kernel<KIND, ASYM, HAS_RES, SPARSE, 2 * NWAVES, 2, ABL>),
