@@ -2,8 +2,9 @@
 // threads: shared by the selection kernel (one group a row) and the sparse
 // decode kernel's selecting prologue (one group a head of its workgroup).
 //
-// A 4-pass radix select (8-bit digits, LDS histograms) finds the n-th
-// largest key of the row; the selected pages are reported in page order,
+// A radix select (8-bit digits, LDS histograms, up to 4 passes: it stops
+// once the threshold digit's bin is taken whole) finds the n-th largest
+// key of the row; the selected pages are reported in page order,
 // ties at the threshold taken in page order (deterministic).  Reference:
 // kernels/cuda/paged_sparse.py:164-168 (select = torch.topk) and the budget
 // rule of kernels/cuda/paged_sparse_fp16.cu:242-247.
@@ -45,7 +46,7 @@ constexpr int SEL_KPT = SELECT_MAX_PAGES / SEL_THREADS;   // keys per thread
 struct SelectSmem {
     uint32_t hist[2][256];
     uint32_t wsum[4];
-    int found[4];
+    int found[6];
 };
 
 // Inclusive prefix sum over the 256 threads of a group (tid: the thread's
@@ -136,31 +137,45 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
         if (ce0 < rem0 && ci0 >= rem0) {
             sm.found[0] = bin;
             sm.found[1] = rem0 - ce0;
+            sm.found[4] = ci0 - ce0;
         }
         if (ce1 < rem1 && ci1 >= rem1) {
             sm.found[2] = bin;
             sm.found[3] = rem1 - ce1;
+            sm.found[5] = ci1 - ce1;
         }
         __syncthreads();
+        // a side is settled once its threshold bin is taken whole: every
+        // key of that prefix is in the set, and no lower digit matters
+        bool fin0 = true, fin1 = true;
         if (rem0 > 0) {
             pre0 |= (uint32_t)sm.found[0] << shift;
             rem0 = sm.found[1];
+            fin0 = rem0 == sm.found[4];
         }
         if (rem1 > 0) {
             pre1 |= (uint32_t)sm.found[2] << shift;
             rem1 = sm.found[3];
+            fin1 = rem1 == sm.found[5];
         }
         msk |= 255u << shift;
-        __syncthreads();
+        // Stop when every group of the workgroup is settled: a workgroup of
+        // several groups (one a head) meets at the same barriers, so the
+        // decision is the whole workgroup's.
+        if (__syncthreads_and(fin0 && fin1)) break;
     }
-    // threshold keys pre0 / pre1; rem0 / rem1 = how many keys equal to them
-    // belong to the set (the lowest pages first)
+    // threshold prefixes pre0 / pre1 of the keys under msk; rem0 / rem1 =
+    // how many keys with that prefix belong to the set (the lowest pages
+    // first; all of them when the passes stopped early)
     const bool want0 = n1 > 0, want1 = n2 > 0;
+    uint32_t kp[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) kp[j] = key[j] & msk;
 
     uint32_t e = 0;
 #pragma unroll
     for (int j = 0; j < KPT; ++j)
-        if (j < cnt) e += (key[j] == pre0 ? 1u : 0u) + (key[j] == pre1 ? 0x10000u : 0u);
+        if (j < cnt) e += (kp[j] == pre0 ? 1u : 0u) + (kp[j] == pre1 ? 0x10000u : 0u);
     uint32_t incl = group_scan(e, sm.wsum, tid);
     uint32_t excl = incl - e;
     int r0 = (int)(excl & 0xFFFFu), r1 = (int)(excl >> 16);
@@ -169,17 +184,17 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
     for (int j = 0; j < KPT; ++j) {
         if (j < cnt) {
             bool a0, a1;
-            if (key[j] == pre0) {
+            if (kp[j] == pre0) {
                 a0 = want0 && r0 < rem0;
                 ++r0;
             } else {
-                a0 = want0 && key[j] > pre0;
+                a0 = want0 && kp[j] > pre0;
             }
-            if (key[j] == pre1) {
+            if (kp[j] == pre1) {
                 a1 = want1 && r1 < rem1;
                 ++r1;
             } else {
-                a1 = want1 && key[j] > pre1;
+                a1 = want1 && kp[j] > pre1;
             }
             ma |= (a0 ? 1u : 0u) << j;
             mb |= (a1 && !a0 ? 1u : 0u) << j;
