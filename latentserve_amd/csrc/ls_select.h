@@ -44,25 +44,33 @@ constexpr int SEL_THREADS = 256;
 constexpr int SEL_KPT = SELECT_MAX_PAGES / SEL_THREADS;   // keys per thread
 
 struct SelectSmem {
-    uint32_t hist[2][256];
-    uint32_t wsum[4];
-    int found[6];
+    uint32_t hist[2][2][256];          // [pass parity][threshold][digit]
+    uint32_t wsum[2][4];               // [scan parity][wave]
+    int found[4];
 };
 
 // Inclusive prefix sum over the 256 threads of a group (tid: the thread's
-// index in its group of 256, whose four waves are whole hardware waves).
+// index in its group of 256, whose four waves are whole hardware waves):
+// DPP row shifts within each row of 16 lanes, readlane for the rows, the
+// four waves' totals through LDS with one barrier.  `wsum` alternates
+// between consecutive calls (a thread may write the next call's totals
+// while another still reads this call's).
 __device__ __forceinline__ uint32_t group_scan(uint32_t v, uint32_t* wsum, int tid) {
     const int lane = tid & 63, wv = tid >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = (uint32_t)__builtin_amdgcn_ds_bpermute((lane - o) << 2, (int)v);
-        if (lane >= o) v += t;
-    }
-    if (lane == 63) wsum[wv] = v;
+    int x = (int)v;
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);   // row_shr:8
+    const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31),
+              r2 = __builtin_amdgcn_readlane(x, 47), r3 = __builtin_amdgcn_readlane(x, 63);
+    const int row = lane >> 4;
+    x += (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+    if (lane == 0) wsum[wv] = (uint32_t)(r0 + r1 + r2 + r3);
     __syncthreads();
-    for (int w = 0; w < wv; ++w) v += wsum[w];
-    __syncthreads();
-    return v;
+    uint32_t u = (uint32_t)x;
+    for (int w = 0; w < wv; ++w) u += wsum[w];
+    return u;
 }
 
 // Select from one row of P scores: out[0, n1) = the n1 best pages, out[n1,
@@ -72,6 +80,9 @@ __device__ __forceinline__ uint32_t group_scan(uint32_t v, uint32_t* wsum, int t
 //
 // KPT keys per thread (P <= 256 * KPT): the loops over a thread's keys are
 // fully unrolled at exactly KPT, so their cost follows the row length.
+//
+// Every group of a workgroup passes the same barriers (a workgroup may run
+// one group a head): three a radix pass, one a scan after them.
 template <bool SORTED, int KPT, class Emit>
 __device__ __attribute__((always_inline)) void select_row_k(const float* srow, int P, int n1,
                                                             int n2, int tid, int32_t* out,
@@ -94,10 +105,11 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
     // ---- radix select of the n1-th and n2-th largest keys ----
     uint32_t pre0 = 0, pre1 = 0, msk = 0;
     int rem0 = n1, rem1 = n2;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        sm.hist[0][tid] = 0;
-        sm.hist[1][tid] = 0;
-        __syncthreads();
+    int nscan = 0;
+    sm.hist[0][0][tid] = 0;
+    sm.hist[0][1][tid] = 0;
+    __syncthreads();
+    for (int shift = 24, par = 0; shift >= 0; shift -= 8, par ^= 1) {
         // A thread's keys are adjacent pages whose leading digits mostly
         // agree (one exponent for the whole row): count runs of equal digits
         // and add each run once, instead of one LDS atomic per key on a
@@ -109,7 +121,7 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
                 const uint32_t d = (key[j] >> shift) & 255u;
                 if ((key[j] & msk) == pre0) {
                     if (d != d0) {
-                        if (n0) atomicAdd(&sm.hist[0][d0], n0);
+                        if (n0) atomicAdd(&sm.hist[par][0][d0], n0);
                         d0 = d;
                         n0 = 0u;
                     }
@@ -117,7 +129,7 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
                 }
                 if ((key[j] & msk) == pre1) {
                     if (d != d1) {
-                        if (n1c) atomicAdd(&sm.hist[1][d1], n1c);
+                        if (n1c) atomicAdd(&sm.hist[par][1][d1], n1c);
                         d1 = d;
                         n1c = 0u;
                     }
@@ -125,44 +137,43 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
                 }
             }
         }
-        if (n0) atomicAdd(&sm.hist[0][d0], n0);
-        if (n1c) atomicAdd(&sm.hist[1][d1], n1c);
+        if (n0) atomicAdd(&sm.hist[par][0][d0], n0);
+        if (n1c) atomicAdd(&sm.hist[par][1][d1], n1c);
+        // the next pass's histogram (last read two barriers ago)
+        sm.hist[par ^ 1][0][tid] = 0;
+        sm.hist[par ^ 1][1][tid] = 0;
         __syncthreads();
         const int bin = 255 - tid;   // thread order = descending digit
-        const uint32_t c = sm.hist[0][bin] | (sm.hist[1][bin] << 16);
-        const uint32_t incl = group_scan(c, sm.wsum, tid);
+        const uint32_t c = sm.hist[par][0][bin] | (sm.hist[par][1][bin] << 16);
+        const uint32_t incl = group_scan(c, sm.wsum[nscan++ & 1], tid);
         const uint32_t excl = incl - c;
         const int ci0 = (int)(incl & 0xFFFFu), ce0 = (int)(excl & 0xFFFFu);
         const int ci1 = (int)(incl >> 16), ce1 = (int)(excl >> 16);
+        // the thread holding a threshold's digit reports it, and whether
+        // that digit's bin is taken whole (then no lower digit matters)
+        bool open = false;
         if (ce0 < rem0 && ci0 >= rem0) {
             sm.found[0] = bin;
             sm.found[1] = rem0 - ce0;
-            sm.found[4] = ci0 - ce0;
+            open = open || rem0 - ce0 != ci0 - ce0;
         }
         if (ce1 < rem1 && ci1 >= rem1) {
             sm.found[2] = bin;
             sm.found[3] = rem1 - ce1;
-            sm.found[5] = ci1 - ce1;
+            open = open || rem1 - ce1 != ci1 - ce1;
         }
-        __syncthreads();
-        // a side is settled once its threshold bin is taken whole: every
-        // key of that prefix is in the set, and no lower digit matters
-        bool fin0 = true, fin1 = true;
+        // the whole workgroup goes on while any of its groups has a side open
+        const bool more = __syncthreads_or(open);
         if (rem0 > 0) {
             pre0 |= (uint32_t)sm.found[0] << shift;
             rem0 = sm.found[1];
-            fin0 = rem0 == sm.found[4];
         }
         if (rem1 > 0) {
             pre1 |= (uint32_t)sm.found[2] << shift;
             rem1 = sm.found[3];
-            fin1 = rem1 == sm.found[5];
         }
         msk |= 255u << shift;
-        // Stop when every group of the workgroup is settled: a workgroup of
-        // several groups (one a head) meets at the same barriers, so the
-        // decision is the whole workgroup's.
-        if (__syncthreads_and(fin0 && fin1)) break;
+        if (!more) break;
     }
     // threshold prefixes pre0 / pre1 of the keys under msk; rem0 / rem1 =
     // how many keys with that prefix belong to the set (the lowest pages
@@ -176,7 +187,7 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
 #pragma unroll
     for (int j = 0; j < KPT; ++j)
         if (j < cnt) e += (kp[j] == pre0 ? 1u : 0u) + (kp[j] == pre1 ? 0x10000u : 0u);
-    uint32_t incl = group_scan(e, sm.wsum, tid);
+    uint32_t incl = group_scan(e, sm.wsum[nscan++ & 1], tid);
     uint32_t excl = incl - e;
     int r0 = (int)(excl & 0xFFFFu), r1 = (int)(excl >> 16);
     uint32_t ma = 0, mb = 0;
@@ -201,7 +212,7 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
         }
     }
     const uint32_t ab = (uint32_t)__builtin_popcount(ma) | ((uint32_t)__builtin_popcount(mb) << 16);
-    incl = group_scan(ab, sm.wsum, tid);
+    incl = group_scan(ab, sm.wsum[nscan++ & 1], tid);
     excl = incl - ab;
     int pa = (int)(excl & 0xFFFFu), pb = n1 + (int)(excl >> 16);
     if constexpr (!SORTED) {
