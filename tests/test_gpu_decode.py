@@ -216,6 +216,23 @@ def test_int8_matches_the_oracle(asym, res, splits):
     assert_close(got.float().cpu().numpy(), want, ATOL, RTOL, f"asym={asym} res={res}")
 
 
+@pytest.mark.parametrize("h_kv", [1, 3, 4])
+@pytest.mark.parametrize("asym", [False, True])
+def test_int8_head_counts(h_kv, asym):
+    """Symmetric pools with an even head count take two heads a workgroup
+    (each head's last page from the residual by its own wave), odd counts
+    and asymmetric pools one: every head's output against the oracle."""
+    (q, k, v, t, l), ex = int8_case([700, 33, 16, 290], asym=asym, res=True, h_kv=h_kv,
+                                    seed=11 + h_kv)
+    want = oracle.paged_decode(q, k, v, t, l, num_splits=1, **ex)
+    Q, K, V, T, L = dev(q, k, v, t, l)
+    dex = {key: dev(val)[0] for key, val in ex.items()}
+    for splits in (None, 5):
+        got = hip_mod().paged_decode_hip(Q, K, V, T, L, 700, num_splits=splits, **dex)
+        torch.cuda.synchronize()
+        assert_close(got.float().cpu().numpy(), want, ATOL, RTOL, f"h_kv={h_kv} splits={splits}")
+
+
 def test_int8_equals_fp16_attention_over_the_dequantised_cache():
     (q, k, v, t, l), ex = int8_case([777, 64], res=True, seed=3)
     kd, vd = dequant_pools(k, v, ex["k_scale"], ex["v_scale"])
