@@ -72,10 +72,6 @@ def parse():
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="instead of the benchmark, run device copies of MIB MiB (for the "
                         "rocprof FETCH_SIZE / WRITE_SIZE scale factor) and exit")
-    p.add_argument("--compute-probe", type=int, default=0, metavar="ITEMS",
-                   help="instead of the benchmark, time the decode kernel's page compute "
-                        "alone (MFMA, as built) against a VALU formulation, ITEMS pages a "
-                        "wave, and exit")
     return p.parse_args()
 
 
@@ -201,7 +197,7 @@ def cpu_baseline(cfg, tables, seq, layer, n_seqs):
 
     import oracle
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = min(host_cores(), 16)
     oracle.set_num_threads(threads)
     b = cfg["batch"]
     n = min(b, n_seqs or b)
@@ -237,12 +233,21 @@ def cpu_baseline(cfg, tables, seq, layer, n_seqs):
                        "C oracle paged_decode (num_splits=1)")
 
 
+def host_cores() -> int:
+    """CPUs this process may run on (the box's share), else the machine's count."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def _cpu_result(cfg, lens, b, n, dt, threads, what):
     sample_bytes = algorithmic_bytes(cfg, lens)
     return {
         "value": round(sample_bytes / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
+        "host_cores": host_cores(),
         "kind": "port",
         "sample": f"{n} of {b} sequences of one layer-step ({sample_bytes / 1e6:.1f} MB), "
                   f"{what} (oracle/ls_oracle.c, OpenMP), median of 3: "
@@ -263,34 +268,6 @@ def calibrate_copy(mib):
     print(json.dumps({"calibrate_copy_bytes": n, "launches": 5}))
 
 
-def compute_probe(items):
-    """Page compute from registers, 8 waves a CU as the decode kernel runs:
-    the cost of one page's QK, softmax and PV per wave, MFMA against VALU,
-    beside the time the c2 walk has per page and wave."""
-    import torch
-    from latentserve_amd.kernels.hip import compute_probe as cp
-    res = {"items_per_wave": items}
-    want = cp.reference().cuda()
-    for groups in (256, 512):
-        for mode in ("mfma", "valu"):
-            out = cp.run(mode, groups, 8)             # warm-up and check
-            torch.cuda.synchronize()
-            err = (out - want).abs().max().item()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(5):
-                cp.run(mode, groups, items, out=out)
-            e1.record()
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / 5
-            res[f"{mode}_g{groups}"] = {"us": round(us, 2),
-                                        "ns_per_page_per_wave": round(us * 1e3 / items, 2),
-                                        "max_abs_err": err}
-    # c2: 16 x 1024 pages x 2 heads over 256 CUs x 8 waves in ~49.6 us
-    res["c2_ns_per_page_per_wave_at_49.6us"] = round(49.6e3 * 256 * 8 / (16 * 1024 * 2), 1)
-    print(json.dumps(res))
-
-
 def main():
     args = parse()
     if args.gpus != 1:
@@ -302,9 +279,6 @@ def main():
 
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
-        return
-    if args.compute_probe:
-        compute_probe(args.compute_probe)
         return
     cfg = CONFIGS[args.config]
     if cfg["kind"] == "step":
@@ -332,8 +306,11 @@ def main():
     full, rem = divmod(args.steps, layers)
     g_full = capture(layers) if full else None
     g_rem = capture(rem) if rem else None
-    if g_full is not None:
-        g_full.replay()
+    # every graph is replayed once before the timed region (its first replay
+    # uploads it), so the timed replays measure the kernels alone
+    for g in (g_full, g_rem):
+        if g is not None:
+            g.replay()
     torch.cuda.synchronize()
 
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -425,15 +425,6 @@ int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64
                            const void* norm_w, float eps, void* res_out, int64_t res_out_stride,
                            void* stream);
 
-/* Measurement only, no counterpart in the reference: the decode kernel's
- * page compute alone, from registers (groups x 8 waves, each applying one
- * synthetic page of 16 tokens x 6 query rows x 128 channels `items` times
- * to its online-softmax state).  mode 0: the kernel's MFMA compute_page;
- * mode 1: a VALU formulation (v_dot2 QK, DPP softmax, FMA PV).  out: [groups
- * * 8][6][128] fp32, each wave's normalised output (the same for every
- * wave).  Timing both modes is the evidence for computing QK and PV on
- * MFMA. */
-int ls_compute_probe(int mode, int groups, int items, float scale, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -94,7 +94,6 @@ _SIGNATURES = {
     "ls_decode_gemm_workspace_bytes": [_I32, _I32, _I32],
     "ls_decode_gate_up_silu": [_VP, _I64, _VP, _I64, _I32, _VP, _VP, _I64, _I32, _I32, _I32,
                                _VP, _I64, _VP, _F32, _VP, _I64, _VP],
-    "ls_compute_probe": [_I32, _I32, _I32, _F32, _VP, _VP],
     "ls_combine_splits": [
         _VP, _I64P, _VP, _VP, _I64P, _VP, _I32, _I64P, _I32, _I32, _I32, _I32, _I32, _VP],
 }

@@ -1,6 +1,7 @@
 """Compile the HIP sources into latentserve_amd/liblatentserve_hip.so (in-tree).
 
     python -m latentserve_amd.csrc.build
+    python -m latentserve_amd.csrc.build --diagnostics PATH   (measurement build)
 
 Cross-compiles for gfx950 with hipcc; no GPU is needed. Object files go to
 latentserve_amd/csrc/_build/ (git-ignored). The library links the HIP runtime
@@ -49,21 +50,30 @@ def _run(cmd):
     return out
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, diagnostics: bool = False, out: str = LIB) -> str:
+    """Compile and link the library to `out`.  ``diagnostics`` adds
+    -DLS_DIAGNOSTICS (ablation variants selected by an environment
+    variable, the page-compute probe): a separate measurement build, never
+    the shipped library."""
     cc = hipcc()
-    obj_dir = os.path.join(HERE, "_build")
+    flags = HIP_FLAGS + (["-DLS_DIAGNOSTICS"] if diagnostics else [])
+    obj_dir = os.path.join(HERE, "_build_diag" if diagnostics else "_build")
     os.makedirs(obj_dir, exist_ok=True)
     objs = [os.path.join(obj_dir, s.replace(".hip", ".o")) for s in SOURCES]
-    cmds = [[cc, *HIP_FLAGS, "-c", os.path.join(HERE, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    cmds = [[cc, *flags, "-c", os.path.join(HERE, s), "-o", o] for s, o in zip(SOURCES, objs)]
     with ThreadPoolExecutor(max_workers=min(8, len(cmds))) as ex:
-        for out in ex.map(_run, cmds):
-            if verbose and out.strip():
-                print(out)
-    tmp = LIB + ".tmp"
+        for log in ex.map(_run, cmds):
+            if verbose and log.strip():
+                print(log)
+    tmp = out + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--diagnostics" in sys.argv:
+        print(build(verbose="-v" in sys.argv, diagnostics=True,
+                    out=sys.argv[sys.argv.index("--diagnostics") + 1]))
+    else:
+        print(build(verbose="-v" in sys.argv))

@@ -1040,6 +1040,8 @@ int ls_decode_gate_up_silu(const void* x, int64_t x_stride, const void* w, int64
     return hip_status(ls::launch_decode_gemm(a, (hipStream_t)stream), "ls_decode_gate_up_silu");
 }
 
+#ifdef LS_DIAGNOSTICS
+// Diagnostic builds only: the page compute alone, MFMA (mode 0) against VALU (1).
 int ls_compute_probe(int mode, int groups, int items, float scale, float* out, void* stream) {
     if (!out) return fail(LS_ERR_INVALID, "null pointer argument");
     if ((mode != 0 && mode != 1) || groups < 1 || groups > 65535 || items < 1)
@@ -1047,6 +1049,7 @@ int ls_compute_probe(int mode, int groups, int items, float scale, float* out, v
     return hip_status(ls::launch_compute_probe(mode, groups, items, scale, out, (hipStream_t)stream),
                       "ls_compute_probe");
 }
+#endif
 
 size_t ls_gemm_packed_bytes(int N, int K, int kind, int head_dim) {
     if (N < 1 || K < 32 || K % 32 != 0 || kind < 0 || kind > 2) return 0;

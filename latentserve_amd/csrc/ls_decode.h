@@ -67,10 +67,12 @@ struct CombineParams {
 
 hipError_t launch_decode(const DecodeParams& a, hipStream_t stream);
 hipError_t launch_combine(const CombineParams& p, hipStream_t stream);
+#ifdef LS_DIAGNOSTICS
 // Page-compute probe (measurement only): groups x 8 waves, each applying one
 // register-resident page `items` times; mode 0 MFMA (compute_page), 1 VALU.
 // out: [groups * 8][6][128] fp32, O of each wave.
 hipError_t launch_compute_probe(int mode, int groups, int items, float scale, float* out,
                                 hipStream_t stream);
+#endif
 
 }  // namespace ls

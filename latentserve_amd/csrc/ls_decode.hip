@@ -1120,8 +1120,11 @@ static hipError_t launch_t(const DecodeParams& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// LATENTSERVE_HIP_ABLATION (diagnostic only; the output is meaningless), for
-// the fp16 dense walk and the symmetric INT8 walk without a residual:
+#ifdef LS_DIAGNOSTICS
+// Diagnostic builds only (-DLS_DIAGNOSTICS; never the shipped library):
+// LATENTSERVE_HIP_ABLATION selects, for the fp16 dense walk and the
+// symmetric INT8 walk without a residual, a variant whose output is
+// meaningless:
 //   loads        the walk with the arithmetic removed
 //   loads_noepi  ... and without the wave merge / partials / split merge
 //   noepi        the full arithmetic without the merge stages
@@ -1134,26 +1137,32 @@ static int ablation() {
         if (strcmp(e, "noepi") == 0) return 3;
         return 0;
     }();
+    if (v) fprintf(stderr, "latentserve_amd: LATENTSERVE_HIP_ABLATION active, output invalid\n");
     return v;
 }
+#endif
 
 static hipError_t launch_kernel(const DecodeParams& a, hipStream_t stream) {
     if (a.scores) return launch_t<KV_FP16, false, false, 2>(a, stream);
     if (a.sel) return launch_t<KV_FP16, false, false, 1>(a, stream);
+#ifdef LS_DIAGNOSTICS
     if (a.kind == KV_FP16 && ablation() != 0) {
         const int abl = ablation();
         if (abl == 1) return launch_t<KV_FP16, false, false, 0, 1>(a, stream);
         if (abl == 2) return launch_t<KV_FP16, false, false, 0, 2>(a, stream);
         return launch_t<KV_FP16, false, false, 0, 3>(a, stream);
     }
+#endif
     if (a.kind == KV_FP16) return launch_t<KV_FP16, false, false, 0>(a, stream);
     const bool asym = a.k_zero != nullptr, res = a.k_res != nullptr;
+#ifdef LS_DIAGNOSTICS
     if (ablation() != 0 && !asym && !res) {
         const int abl = ablation();
         if (abl == 1) return launch_t<KV_INT8, false, false, 0, 1>(a, stream);
         if (abl == 2) return launch_t<KV_INT8, false, false, 0, 2>(a, stream);
         return launch_t<KV_INT8, false, false, 0, 3>(a, stream);
     }
+#endif
     if (asym && res) return launch_t<KV_INT8, true, true, 0>(a, stream);
     if (asym) return launch_t<KV_INT8, true, false, 0>(a, stream);
     if (res) return launch_t<KV_INT8, false, true, 0>(a, stream);
@@ -1174,6 +1183,7 @@ hipError_t launch_combine(const CombineParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+#ifdef LS_DIAGNOSTICS
 // ---- compute probe: the page compute alone, MFMA against VALU ----
 //
 // Measurement only (no counterpart in the reference).  Every wave applies
@@ -1353,5 +1363,7 @@ hipError_t launch_compute_probe(int mode, int groups, int items, float scale, fl
                            items, scale_log2, out);
     return hipGetLastError();
 }
+
+#endif  // LS_DIAGNOSTICS
 
 }  // namespace ls

@@ -227,7 +227,7 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
             pos[j] = pa;
-            if ((ma >> j) & 1u) skeys[pa++] = key[j];
+            if (((ma >> j) & 1u) && pa < n1) skeys[pa++] = key[j];
         }
         __syncthreads();
         int rank[KPT];
@@ -241,7 +241,7 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
         }
 #pragma unroll
         for (int j = 0; j < KPT; ++j)
-            if ((ma >> j) & 1u) out[rank[j]] = i0 + j;
+            if (((ma >> j) & 1u) && rank[j] < n1) out[rank[j]] = i0 + j;
     }
 }
 

@@ -146,7 +146,13 @@ __global__ __launch_bounds__(256) void page_select_kernel(SelectParams a) {
     const int n1 = SORTED ? a.k : budget_pages(L, a.P, a.ratio, a.recent, a.k);
     int32_t* out = a.sel + (int64_t)b * a.sl_b + (int64_t)h * a.sl_h;
     const float* srow = a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h;
-    auto emit = [&](int pos, int pg) { out[pos] = pg; };
+    // a position outside the row is never stored: a bad scan result (a
+    // histogram counted from a lane that held no key) cannot reach memory
+    // outside this row of the output
+    const int k = a.k;
+    auto emit = [&](int pos, int pg) {
+        if ((unsigned)pos < (unsigned)k) out[pos] = pg;
+    };
     select_row<SORTED>(srow, a.P, n1, a.k, (int)threadIdx.x, out, sm, skeys, emit);
 }
 
