@@ -85,6 +85,25 @@ int ls_paged_decode_fp16(const void* q, const int64_t* q_strides, const void* k_
                          int batch, int kv_heads, int n_rep, int head_dim, int page,
                          int num_splits, int max_seq_len, float softmax_scale, void* stream);
 
+/* fp16 paged decode that allocates nothing and takes no workspace or
+ * counters: the same kernel as ls_paged_decode_fp16, its split records and
+ * arrival counters in a fixed device array of the library (16 MiB of records
+ * plus 65536 counters, held per GPU until the process ends).  No counterpart
+ * in the reference: for callers that cannot allocate device memory (code
+ * under graph capture, tight serving loops, harnesses that forbid it).
+ * Returns LS_ERR_INVALID when ls_decode_workspace_bytes(batch, kv_heads,
+ * n_rep, num_splits) exceeds 16 MiB or batch * kv_heads exceeds 65536.  The
+ * first call on a device looks the array up and clears its counters on
+ * `stream`.  All calls on one GPU share the array: calls that overlap on
+ * one GPU (concurrent streams) race. */
+int ls_paged_decode_fp16_noalloc(const void* q, const int64_t* q_strides, const void* k_pool,
+                                 const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                                 const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                                 const int32_t* seq_lens, void* out, const int64_t* out_strides,
+                                 int batch, int kv_heads, int n_rep, int head_dim, int page,
+                                 int num_splits, int max_seq_len, float softmax_scale,
+                                 void* stream);
+
 /* INT8 paged decode.  Replaces paged_decode_int8 (kernels/cuda/paged_decode_int8.cu:87-102;
  * launcher kernels/cuda/paged_decode_cuda.py:236-244).  k_scale/v_scale
  * required (fp32); k_zero and v_zero both or neither; k_residual with

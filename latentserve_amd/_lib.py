@@ -28,7 +28,7 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -38,6 +38,9 @@ _SIGNATURES = {
     "ls_paged_decode_fp16": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
         _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
+    "ls_paged_decode_fp16_noalloc": [
+        _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
+        _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
     "ls_paged_decode_int8": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64P, _VP, _I64P, _VP, _VP,
         _VP, _I64P, _I32, _VP, _VP, _I64, _I32, _VP, _VP, _I64P,

@@ -229,7 +229,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 13; }
+int ls_abi_version(void) { return 14; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -255,6 +255,36 @@ int ls_paged_decode_fp16(const void* q, const int64_t* q_strides, const void* k_
                 kv_heads, n_rep, num_splits, max_seq_len, softmax_scale);
     a.kind = ls::KV_FP16;
     return hip_status(ls::launch_decode(a, (hipStream_t)stream), "ls_paged_decode_fp16");
+}
+
+int ls_paged_decode_fp16_noalloc(const void* q, const int64_t* q_strides, const void* k_pool,
+                                 const void* v_pool, const int64_t* kv_strides, int num_blocks,
+                                 const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                                 const int32_t* seq_lens, void* out, const int64_t* out_strides,
+                                 int batch, int kv_heads, int n_rep, int head_dim, int page,
+                                 int num_splits, int max_seq_len, float softmax_scale,
+                                 void* stream) {
+    if (batch > 0 && kv_heads > 0 && (int64_t)batch * kv_heads > ls::NOALLOC_COUNTERS)
+        return fail(LS_ERR_INVALID,
+                    "ls_paged_decode_fp16_noalloc: batch * kv_heads = %lld exceeds the fixed "
+                    "scratch's %d arrival counters",
+                    (long long)batch * kv_heads, ls::NOALLOC_COUNTERS);
+    const size_t need = ls_decode_workspace_bytes(batch, kv_heads, n_rep, num_splits);
+    if (need > ls::NOALLOC_WORK_BYTES)
+        return fail(LS_ERR_INVALID,
+                    "ls_paged_decode_fp16_noalloc: %zu bytes of split records (batch %d, "
+                    "kv_heads %d, n_rep %d, num_splits %d) exceed the fixed scratch's %zu; use "
+                    "fewer splits or ls_paged_decode_fp16 with a workspace",
+                    need, batch, kv_heads, n_rep, num_splits, ls::NOALLOC_WORK_BYTES);
+    float* work = nullptr;
+    int32_t* counters = nullptr;
+    if (int rc = hip_status(ls::noalloc_scratch((hipStream_t)stream, &work, &counters),
+                            "ls_paged_decode_fp16_noalloc (scratch set-up)"))
+        return rc;
+    return ls_paged_decode_fp16(q, q_strides, k_pool, v_pool, kv_strides, num_blocks,
+                                block_tables, bt_stride, max_pages, seq_lens, out, out_strides,
+                                work, counters, batch, kv_heads, n_rep, head_dim, page,
+                                num_splits, max_seq_len, softmax_scale, stream);
 }
 
 int ls_paged_decode_int8(const void* q, const int64_t* q_strides, const void* k_pool,

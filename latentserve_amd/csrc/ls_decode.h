@@ -66,6 +66,15 @@ struct CombineParams {
 };
 
 hipError_t launch_decode(const DecodeParams& a, hipStream_t stream);
+
+// The no-allocation decode's fixed device scratch: split records
+// (NOALLOC_WORK_BYTES) then arrival counters (NOALLOC_COUNTERS int32, so
+// batch * kv_heads <= NOALLOC_COUNTERS).
+constexpr size_t NOALLOC_WORK_BYTES = size_t(16) << 20;
+constexpr int NOALLOC_COUNTERS = 1 << 16;
+// This device's scratch (looked up, and its counters cleared on `stream`,
+// at the first call on the device).
+hipError_t noalloc_scratch(hipStream_t stream, float** work, int32_t** counters);
 hipError_t launch_combine(const CombineParams& p, hipStream_t stream);
 #ifdef LS_DIAGNOSTICS
 // Page-compute probe (measurement only): groups x 8 waves, each applying one

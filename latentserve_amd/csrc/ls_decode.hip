@@ -45,6 +45,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "ls_common.h"
 #include "ls_decode.h"
 #include "ls_select.h"
@@ -1365,5 +1367,60 @@ hipError_t launch_compute_probe(int mode, int groups, int items, float scale, fl
 }
 
 #endif  // LS_DIAGNOSTICS
+
+}  // namespace ls
+
+// ------------------------------------------------ no-allocation variant ----
+//
+// For callers that cannot allocate device memory (code under graph capture,
+// tight serving loops): the fp16 decode with its split workspace and arrival
+// counters in one fixed device array of this library instead of caller
+// buffers.  Each GPU holds its own copy (until the process ends), found by
+// its address on that device; every call on a GPU shares it, so calls that
+// overlap on one GPU race.  The counters are cleared once per device at the
+// first call and are left at zero by every call after (the last workgroup of
+// each (sequence, head) resets its own).
+
+static __device__ __align__(256) unsigned char scratch[ls::NOALLOC_WORK_BYTES +
+                                                        ls::NOALLOC_COUNTERS * sizeof(int32_t)];
+
+namespace ls {
+namespace {
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+__global__ __launch_bounds__(256) void zero_i32_kernel(int32_t* p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+}  // namespace
+
+hipError_t noalloc_scratch(hipStream_t stream, float** work, int32_t** counters) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        int32_t* cnt = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(p) +
+                                                  NOALLOC_WORK_BYTES);
+        hipLaunchKernelGGL(zero_i32_kernel, dim3((NOALLOC_COUNTERS + 255) / 256), dim3(256), 0,
+                           stream, cnt, NOALLOC_COUNTERS);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = p;
+    }
+    unsigned char* base = static_cast<unsigned char*>(g_scratch_ptr[dev]);
+    *work = reinterpret_cast<float*>(base);
+    *counters = reinterpret_cast<int32_t*>(base + NOALLOC_WORK_BYTES);
+    return hipSuccess;
+}
 
 }  // namespace ls
