@@ -31,6 +31,7 @@ from latentserve_amd.kernels import decode_gemm as dg
 from latentserve_amd.kernels import fused_elementwise as fe
 from latentserve_amd.kernels.hip import paged_decode_hip as pdh
 from latentserve_amd.kernels.hip import paged_sparse as ps
+from latentserve_amd.runtime.int8_cache import Int8PagedKVCache
 from latentserve_amd.runtime.kv_cache import KVCacheSpec, PagedKVCache
 
 
@@ -151,23 +152,44 @@ class QwenDecoder:
             torch.randn(cfg.vocab_size, cfg.hidden_size, generator=gen, device=self.device)
             * std).to(torch.float16)
         self.p_lm_head = _pack(self.lm_head, "plain")
-        self.cache: Optional[PagedKVCache] = None
+        self.cache = None
+        self._stage = None
         self.rope: Optional[Rope] = None
         self.sparse_ratio: Optional[float] = None
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
 
     def allocate_cache(self, max_batch_size: int, max_seq_len: int,
-                       num_blocks: Optional[int] = None) -> PagedKVCache:
+                       num_blocks: Optional[int] = None, kv_dtype: str = "fp16",
+                       asymmetric: bool = False):
+        """A paged cache for this model: fp16 (PagedKVCache) or INT8
+        (Int8PagedKVCache: int8 pools, fp32 scales, the fp16 last-page K
+        residual)."""
         spec = KVCacheSpec(num_layers=self.cfg.num_layers, num_kv_heads=self.cfg.num_kv_heads,
                            head_dim=self.cfg.head_dim, max_batch_size=max_batch_size,
                            max_seq_len=max_seq_len, device=str(self.device))
-        self.cache = PagedKVCache(spec, num_blocks=num_blocks)
+        if kv_dtype == "fp16":
+            self.cache = PagedKVCache(spec, num_blocks=num_blocks)
+            self._stage = None
+        elif kv_dtype == "int8":
+            self.cache = Int8PagedKVCache(spec, num_blocks=num_blocks, asymmetric=asymmetric)
+            # the decode token's rotated K and its V are stored here by the
+            # q/k/v launch (one 16-row block per sequence, row 0), then
+            # quantized into the cache by its write
+            hk, hd = self.cfg.num_kv_heads, self.cfg.head_dim
+            self._stage = (
+                torch.zeros(max_batch_size, 16, hk, hd, dtype=torch.float16, device=self.device),
+                torch.zeros(max_batch_size, 16, hk, hd, dtype=torch.float16, device=self.device),
+                torch.arange(max_batch_size, dtype=torch.long, device=self.device) * 16)
+        else:
+            raise ValueError(f"kv_dtype must be 'fp16' or 'int8', got {kv_dtype!r}")
         self.rope = Rope(self.cfg.head_dim, self.cfg.rope_theta, max_seq_len, self.device)
         return self.cache
 
     def set_sparse(self, ratio: Optional[float], recent: int = 2) -> None:
         """Sparse decode attention over a page budget (None: dense)."""
         if ratio is not None:
+            if isinstance(self.cache, Int8PagedKVCache):
+                raise ValueError("sparse decode reads fp16 pools; this cache is INT8")
             self.cache.enable_page_bounds()
         self.sparse_ratio = ratio
         for layer in self.layers:
@@ -185,7 +207,13 @@ class QwenDecoder:
         eps = cfg.rms_norm_eps
         tables = cache.block_tables_tensor(b)
         lens = cache.seq_lens_tensor(b)
-        slots = cache.write_slots(b)
+        int8 = self._stage is not None
+        if int8:
+            stage_k, stage_v, stage_slots = self._stage
+            slots = stage_slots[:b]
+            res_rows = cache.residual_rows_tensor(b)
+        else:
+            slots = cache.write_slots(b)
         pos = positions.reshape(b)
         q = torch.empty((b, hk, hq // hk, hd), dtype=torch.float16, device=self.device)
         o = torch.empty_like(q)                                    # = [B, hq * hd], contiguous
@@ -211,21 +239,31 @@ class QwenDecoder:
             # (and the page bounds) and q folded to [B, hk, n_rep, hd]: one
             # launch at decode batch sizes (the projection's epilogue)
             wq = layer.p_qkv if layer.p_qkv is not None else layer.w_qkv
+            kdst, vdst = (stage_k, stage_v) if int8 else (cache.k_pool[li], cache.v_pool[li])
             if fold1:
                 _, residual = dg.qkv_rope_write(
                     x, wq, layer.b_qkv, pos, self.rope.cos, self.rope.sin, slots,
-                    cache.k_pool[li], cache.v_pool[li], hq, hk, q_out=q, kmin=kmin, kmax=kmax,
+                    kdst, vdst, hq, hk, q_out=q, kmin=kmin, kmax=kmax,
                     residual=residual, norm_weight=layer.norm1, eps=eps)
             elif b <= HIP_GEMM_MAX_ROWS and dg.supports(h, wq):
                 dg.qkv_rope_write(h, wq, layer.b_qkv, pos, self.rope.cos, self.rope.sin,
-                                  slots, cache.k_pool[li], cache.v_pool[li], hq, hk, q_out=q,
-                                  kmin=kmin, kmax=kmax)
+                                  slots, kdst, vdst, hq, hk, q_out=q, kmin=kmin, kmax=kmax)
             else:
                 qkv = F.linear(h, layer.w_qkv, layer.b_qkv)       # [B, (hq + 2 hk) hd]
                 fe.rope_write_decode(qkv, pos, self.rope.cos, self.rope.sin, slots,
-                                     cache.k_pool[li], cache.v_pool[li], hq, hk, q_out=q,
-                                     kmin=kmin, kmax=kmax)
-            if self.sparse_ratio is None:
+                                     kdst, vdst, hq, hk, q_out=q, kmin=kmin, kmax=kmax)
+            if int8:
+                # V quantized into the pool, K into the sequence's residual row
+                cache.write(li, stage_k[:b, :1].transpose(1, 2), stage_v[:b, :1].transpose(1, 2))
+                pdh.paged_decode_hip(
+                    q, cache.k_pool[li], cache.v_pool[li], tables, lens,
+                    max_seq_len=max_position + 1, num_splits=layer.attn.num_splits,
+                    softmax_scale=self.scale, k_scale=cache.k_scale_pool[li],
+                    v_scale=cache.v_scale_pool[li],
+                    k_zero=cache.k_zero_pool[li] if cache.asymmetric else None,
+                    v_zero=cache.v_zero_pool[li] if cache.asymmetric else None,
+                    k_residual=cache.residual(li), res_rows=res_rows, out=o)
+            elif self.sparse_ratio is None:
                 pdh.paged_decode_hip(q, cache.k_pool[li], cache.v_pool[li], tables, lens,
                                      max_seq_len=max_position + 1,
                                      num_splits=layer.attn.num_splits,

@@ -61,7 +61,7 @@ def test_advance_keeps_persistent_capacity_width_buffers():
     c = _cache()
     c.advance(20, batch_size=2)
     bt, sl = c.block_tables_tensor(), c.seq_lens_tensor()
-    base = c._block_tables_buf.data_ptr()
+    base = c.inputs.tables.data_ptr()
     assert bt.shape == (2, 7) and sl.tolist() == [20, 20]
     assert bt.data_ptr() == base
     c.advance(1, slots=[1, 0])
@@ -69,7 +69,8 @@ def test_advance_keeps_persistent_capacity_width_buffers():
     assert c.block_tables_tensor().data_ptr() == base
     rows = c.block_tables_tensor()
     assert rows[0, :2].tolist() == c.tables[1].blocks and rows[1, :2].tolist() == c.tables[0].blocks
-    assert c._write_slots.tolist() == [[c.tables[1].slot(20)], [c.tables[0].slot(20)]]
+    assert c.write_slots(2).tolist() == [c.tables[1].slot(20), c.tables[0].slot(20)]
+    assert c.write_slots(2).data_ptr() == c.inputs.vec["write_slot"].data_ptr()
 
 
 def test_write_scatters_to_the_advanced_slots():
@@ -82,9 +83,28 @@ def test_write_scatters_to_the_advanced_slots():
     for b in range(2):
         for p in range(5):
             s = c.tables[b].slot(p)
-            assert torch.equal(c._flat_k[1][s], k[b, :, p])
-            assert torch.equal(c._flat_v[1][s], v[b, :, p])
-    assert c._flat_k[0].abs().sum() == 0
+            assert torch.equal(c.k_pool[1].view(-1, 2, 128)[s], k[b, :, p])
+            assert torch.equal(c.v_pool[1].view(-1, 2, 128)[s], v[b, :, p])
+    assert c.k_pool[0].abs().sum() == 0
+
+
+def test_table_rows_follow_slot_reuse_and_growth():
+    """A row reassigned to another sequence is rewritten whole; a row whose
+    sequence only grew gets its new entries; a freed-and-refilled slot is
+    never served its old blocks."""
+    c = _cache(batch=2, cap=200)
+    c.advance(40, batch_size=2)                         # 3 pages each
+    c.advance(1, slots=[1])                             # row 0 now holds slot 1
+    assert c.block_tables_tensor(1)[0, :3].tolist() == c.tables[1].blocks
+    c.free_sequence(0)
+    c.advance(33, slots=[0])                            # slot 0 refilled: LIFO blocks
+    assert c.block_tables_tensor(1)[0, :3].tolist() == c.tables[0].blocks
+    for _ in range(20):                                 # grows by one page
+        c.advance(1, slots=[0, 1])
+    rows = c.block_tables_tensor(2)
+    for r, s in enumerate([0, 1]):
+        assert rows[r, :len(c.tables[s].blocks)].tolist() == c.tables[s].blocks
+    assert c.seq_lens_tensor().tolist() == [53, 61]
 
 
 def test_capacity_is_enforced_and_rewind_keeps_blocks():
