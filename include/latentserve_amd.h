@@ -186,6 +186,26 @@ int ls_page_scores(const void* q, const int64_t* q_strides, const void* kmin, co
                    const int64_t* score_strides, int batch, int kv_heads, int n_rep, int head_dim,
                    int page, int recent, void* stream);
 
+/* Bytes of `workspace` ls_page_scores_mass needs: the per-head logits,
+ * fp32 [batch, kv_heads, n_rep, max_pages]. */
+size_t ls_page_mass_workspace_bytes(int batch, int kv_heads, int n_rep, int max_pages);
+
+/* Summed-mass page scores [B, H, 0:max_pages] fp32.  Replaces
+ * page_scores_mass (kernels/cuda/paged_sparse.py:126-161, with the
+ * page_index_heads kernel, kernels/cuda/paged_sparse_fp16.cu:141-190): each
+ * query head's Quest bound of a page turned into an estimated attention
+ * weight, softmax over the row's pages of bound * softmax_scale +
+ * log(tokens in the page), summed over the KV head's query heads; page 0
+ * and the last `recent` pages +inf, pages past the end -inf.  Two launches
+ * (per-head logits into `workspace`, then the row softmaxes). */
+int ls_page_scores_mass(const void* q, const int64_t* q_strides, const void* kmin,
+                        const void* kmax, const int64_t* bound_strides, int num_blocks,
+                        const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                        const int32_t* seq_lens, float* workspace, float* scores,
+                        const int64_t* score_strides, int batch, int kv_heads, int n_rep,
+                        int head_dim, int page, int recent, float softmax_scale,
+                        void* stream);
+
 /* Top-k pages per (sequence, KV head) from scores [.., 0:num_pages].
  * Replaces select (kernels/cuda/paged_sparse.py:164-168, torch.topk).
  * Order of equal scores: lower page first.  sorted = 1: sel[0:k] best

@@ -28,7 +28,7 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -41,6 +41,10 @@ _SIGNATURES = {
     "ls_paged_decode_fp16_noalloc": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
+    "ls_page_mass_workspace_bytes": [_I32, _I32, _I32, _I32],
+    "ls_page_scores_mass": [
+        _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _VP, _I64P, _I32, _I32,
+        _I32, _I32, _I32, _I32, _F32, _VP],
     "ls_paged_decode_int8": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64P, _VP, _I64P, _VP, _VP,
         _VP, _I64P, _I32, _VP, _VP, _I64, _I32, _VP, _VP, _I64P,
@@ -128,6 +132,7 @@ def lib() -> ctypes.CDLL:
                           "ls_decode_workspace_bytes": ctypes.c_size_t,
                           "ls_decode_gemm_workspace_bytes": ctypes.c_size_t,
                           "ls_argmax_workspace_bytes": ctypes.c_size_t,
+                          "ls_page_mass_workspace_bytes": ctypes.c_size_t,
                           "ls_gemm_packed_bytes": ctypes.c_size_t}.get(name, ctypes.c_int)
         got = handle.ls_abi_version()
         if got != ABI_VERSION:

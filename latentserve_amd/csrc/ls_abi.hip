@@ -229,7 +229,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 14; }
+int ls_abi_version(void) { return 15; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -461,6 +461,65 @@ int ls_page_scores(const void* q, const int64_t* q_strides, const void* kmin, co
                            stream);
 }
 
+size_t ls_page_mass_workspace_bytes(int batch, int kv_heads, int n_rep, int max_pages) {
+    if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || max_pages <= 0) return 0;
+    return (size_t)batch * kv_heads * n_rep * max_pages * sizeof(float);
+}
+
+int ls_page_scores_mass(const void* q, const int64_t* q_strides, const void* kmin,
+                        const void* kmax, const int64_t* bound_strides, int num_blocks,
+                        const int32_t* block_tables, int64_t bt_stride, int max_pages,
+                        const int32_t* seq_lens, float* workspace, float* scores,
+                        const int64_t* score_strides, int batch, int kv_heads, int n_rep,
+                        int head_dim, int page, int recent, float softmax_scale,
+                        void* stream) {
+    if (!q || !q_strides || !kmin || !kmax || !bound_strides || !block_tables || !seq_lens ||
+        !scores || !score_strides || !workspace)
+        return fail(LS_ERR_INVALID, "null pointer argument");
+    if (head_dim != ls::HEAD_DIM) return fail(LS_ERR_INVALID, "head_dim must be 128, got %d", head_dim);
+    if (page != ls::PAGE) return fail(LS_ERR_INVALID, "page (block_size) must be 16, got %d", page);
+    if (n_rep < 1 || n_rep > ls::MAX_NREP)
+        return fail(LS_ERR_INVALID, "n_rep must be in [1, %d], got %d", ls::MAX_NREP, n_rep);
+    if (batch < 0 || batch > 65535 || kv_heads < 1 || kv_heads > 65535)
+        return fail(LS_ERR_INVALID, "bad batch (%d) or kv_heads (%d)", batch, kv_heads);
+    if (num_blocks < 0 || max_pages < 0 || recent < 0)
+        return fail(LS_ERR_INVALID, "bad num_blocks, max_pages or recent");
+    if (!rows_aligned(q, q_strides, 3, 2, 16))
+        return fail(LS_ERR_INVALID, "q rows must be 16-byte aligned");
+    if (!rows_aligned(kmin, bound_strides, 2, 2, 16) || !rows_aligned(kmax, bound_strides, 2, 2, 16))
+        return fail(LS_ERR_INVALID, "kmin/kmax rows must be 16-byte aligned");
+    if (!aligned(scores, 4) || !aligned(workspace, 4))
+        return fail(LS_ERR_INVALID, "scores and workspace must be 4-byte aligned");
+    if (batch == 0 || max_pages == 0) return LS_OK;
+    ls::IndexParams a{};
+    a.q = q;
+    a.sq_b = q_strides[0];
+    a.sq_h = q_strides[1];
+    a.sq_r = q_strides[2];
+    a.kmin = kmin;
+    a.kmax = kmax;
+    a.sb_b = bound_strides[0];
+    a.sb_h = bound_strides[1];
+    a.num_blocks = num_blocks;
+    a.block_tables = block_tables;
+    a.sbt_b = bt_stride;
+    a.max_pages = max_pages;
+    a.seq_lens = seq_lens;
+    a.scores = scores;
+    a.ss_b = score_strides[0];
+    a.ss_h = score_strides[1];
+    a.B = batch;
+    a.H = kv_heads;
+    a.NR = n_rep;
+    a.recent = recent;
+    a.heads = workspace;                  // [B, H, NR, max_pages], contiguous
+    a.sh_r = max_pages;
+    a.sh_h = (int64_t)n_rep * max_pages;
+    a.sh_b = (int64_t)kv_heads * a.sh_h;
+    a.scale_log2 = softmax_scale * 1.4426950408889634f;
+    return hip_status(ls::launch_page_mass(a, (hipStream_t)stream), "ls_page_scores_mass");
+}
+
 int ls_sparse_index(const void* q, const int64_t* q_strides, const void* kmin, const void* kmax,
                     const int64_t* bound_strides, int num_blocks, const int32_t* block_tables,
                     int64_t bt_stride, int max_pages, const int32_t* seq_lens, float* scores,
@@ -494,7 +553,7 @@ int ls_sparse_index(const void* q, const int64_t* q_strides, const void* kmin, c
                         ls::SELECT_MAX_PAGES, max_pages);
     }
     if (batch == 0 || max_pages == 0) return LS_OK;
-    ls::IndexParams a;
+    ls::IndexParams a{};
     a.q = q;
     a.sq_b = q_strides[0];
     a.sq_h = q_strides[1];

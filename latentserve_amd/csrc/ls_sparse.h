@@ -27,6 +27,10 @@ struct IndexParams {
     float* scores;          // fp32 [B, H, >= max_pages]
     int64_t ss_b, ss_h;
     int B, H, NR, recent;
+    // summed-mass scoring only: per-head logits fp32 [B, H, NR, >= max_pages]
+    float* heads;
+    int64_t sh_b, sh_h, sh_r;
+    float scale_log2;       // softmax scale * log2(e)
 };
 
 struct SelectParams {
@@ -51,6 +55,8 @@ struct BoundsParams {
 
 hipError_t launch_page_index(const IndexParams& p, hipStream_t stream);
 hipError_t launch_page_select(const SelectParams& p, hipStream_t stream);
+// Summed-mass scores: the per-head index launch, then the row softmaxes.
+hipError_t launch_page_mass(const IndexParams& p, hipStream_t stream);
 hipError_t launch_bounds_update(const BoundsParams& p, hipStream_t stream);
 hipError_t launch_bounds_rebuild(const BoundsParams& p, hipStream_t stream);
 

@@ -68,7 +68,12 @@ __device__ __forceinline__ void h8_to_f8(u4 x, float* f) {
 
 // NR: query rows per KV head (a compile-time count keeps only those rows'
 // registers, which sets how many index groups a CU holds at once).
-template <int NR>
+// MASS: instead of the group's max bound, write every query head's bound as
+// a log2-domain logit, bound * scale * log2(e) + log2(tokens in the page),
+// to heads[b, h, r, p] (sink and recent pages scored like the others, pages
+// past the end or with a block id outside the pool -inf); page_mass_kernel
+// turns them into the summed-mass scores.
+template <int NR, bool MASS = false>
 __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
     const int b = blockIdx.z, h = blockIdx.y;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -89,7 +94,7 @@ __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
             st[i] = PG_SKIP;
         } else if (p >= np) {
             st[i] = PG_PAST;
-        } else if (p == 0 || p >= np - a.recent) {
+        } else if (!MASS && (p == 0 || p >= np - a.recent)) {
             st[i] = PG_FORCED;
         } else {
             const int blk = a.block_tables[(int64_t)b * a.sbt_b + p];
@@ -123,9 +128,27 @@ __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) s += fmaxf(qf[j] * lf[j], qf[j] * hf[j]);
             s = row16_sum(s);
-            bst = fmaxf(bst, s);
+            if (MASS)
+                bst = (lane & 15) == r ? s : bst;    // lane r of the row keeps head r
+            else
+                bst = fmaxf(bst, s);
         }
         best[i] = bst;
+    }
+    if constexpr (MASS) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = lane & 15;
+            if (r < NR && st[i] != PG_SKIP) {
+                float v = neg_inf();
+                if (st[i] == PG_SCORE) {
+                    const int cnt = min(PAGE, L - pg[i] * PAGE);
+                    v = best[i] * a.scale_log2 + __log2f((float)cnt);
+                }
+                a.heads[(int64_t)b * a.sh_b + (int64_t)h * a.sh_h + (int64_t)r * a.sh_r + pg[i]] = v;
+            }
+        }
+        return;
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -134,6 +157,78 @@ __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
                             : st[i] == PG_FORCED ? __builtin_inff() : neg_inf();
             a.scores[(int64_t)b * a.ss_b + (int64_t)h * a.ss_h + pg[i]] = v;
         }
+    }
+}
+
+// Summed-mass page scores from the per-head logits (one 256-thread group
+// per (sequence, KV head) row): for each query head a softmax over the
+// row's pages of its log2-domain logits, the softmaxes summed over the
+// group's heads; sink and recent pages +inf, pages past the end -inf
+// (kernels/cuda/paged_sparse.py:126-161).  Three passes over the row's
+// NR x P logits (just written, cache-resident): maxima, sums, scores.
+template <int NR>
+__global__ __launch_bounds__(256) void page_mass_kernel(IndexParams a) {
+    __shared__ float red[4][NR];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
+    const int L = a.seq_lens[b];
+    const int np = L > 0 ? (L + PAGE - 1) / PAGE : 0;
+    const int P = a.max_pages;
+    const float* row = a.heads + (int64_t)b * a.sh_b + (int64_t)h * a.sh_h;
+    float* out = a.scores + (int64_t)b * a.ss_b + (int64_t)h * a.ss_h;
+
+    auto group_reduce = [&](float (&v)[NR], bool is_max) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float o = __shfl_xor(v[r], off);
+                v[r] = is_max ? fmaxf(v[r], o) : v[r] + o;
+            }
+        }
+        __syncthreads();                    // red[] free (read by the last reduction)
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) red[wv][r] = v[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const float x0 = red[0][r], x1 = red[1][r], x2 = red[2][r], x3 = red[3][r];
+            v[r] = is_max ? fmaxf(fmaxf(x0, x1), fmaxf(x2, x3)) : (x0 + x1) + (x2 + x3);
+        }
+    };
+
+    float mx[NR], sm[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) mx[r] = neg_inf();
+    for (int p = tid; p < P; p += 256)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) mx[r] = fmaxf(mx[r], row[(int64_t)r * a.sh_r + p]);
+    group_reduce(mx, true);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        sm[r] = 0.f;
+        mx[r] = mx[r] == neg_inf() ? 0.f : mx[r];   // an empty row: every weight 0
+    }
+    for (int p = tid; p < P; p += 256)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) sm[r] += exp2f(row[(int64_t)r * a.sh_r + p] - mx[r]);
+    group_reduce(sm, false);
+    float inv[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) inv[r] = sm[r] > 0.f ? 1.f / sm[r] : 0.f;
+    for (int p = tid; p < P; p += 256) {
+        float v;
+        if (p >= np) {
+            v = neg_inf();
+        } else if (p == 0 || p >= np - a.recent) {
+            v = __builtin_inff();
+        } else {
+            v = 0.f;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) v += exp2f(row[(int64_t)r * a.sh_r + p] - mx[r]) * inv[r];
+        }
+        out[p] = v;
     }
 }
 
@@ -235,6 +330,24 @@ hipError_t launch_page_index(const IndexParams& p, hipStream_t stream) {
         LS_INDEX_NR(7) LS_INDEX_NR(8) LS_INDEX_NR(9) LS_INDEX_NR(10) LS_INDEX_NR(11)
         LS_INDEX_NR(12) LS_INDEX_NR(13) LS_INDEX_NR(14) LS_INDEX_NR(15) LS_INDEX_NR(16)
 #undef LS_INDEX_NR
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_page_mass(const IndexParams& p, hipStream_t stream) {
+    if (p.B == 0 || p.max_pages == 0) return hipSuccess;
+    const dim3 grid((p.max_pages + INDEX_PAGES_PER_GROUP - 1) / INDEX_PAGES_PER_GROUP, p.H, p.B);
+    switch (p.NR) {
+#define LS_MASS_NR(n)                                                                      \
+    case n:                                                                                \
+        hipLaunchKernelGGL((page_index_kernel<n, true>), grid, dim3(256), 0, stream, p);   \
+        hipLaunchKernelGGL(page_mass_kernel<n>, dim3(p.H, p.B), dim3(256), 0, stream, p);  \
+        break;
+        LS_MASS_NR(1) LS_MASS_NR(2) LS_MASS_NR(3) LS_MASS_NR(4) LS_MASS_NR(5) LS_MASS_NR(6)
+        LS_MASS_NR(7) LS_MASS_NR(8) LS_MASS_NR(9) LS_MASS_NR(10) LS_MASS_NR(11)
+        LS_MASS_NR(12) LS_MASS_NR(13) LS_MASS_NR(14) LS_MASS_NR(15) LS_MASS_NR(16)
+#undef LS_MASS_NR
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -105,6 +105,31 @@ def page_scores(q, kmin, kmax, block_tables, seq_lens, recent: int = 2) -> torch
     return scores
 
 
+def page_scores_mass(q, kmin, kmax, block_tables, seq_lens, recent: int = 2,
+                     softmax_scale: Optional[float] = None, page: int = PAGE) -> torch.Tensor:
+    """Summed-mass scores -> [B, H, max_pages] fp32 (kernels/cuda/
+    paged_sparse.py:126-161): for each query head a softmax over the pages
+    of bound * scale + log(tokens in the page), summed over the group; page
+    0 and the last `recent` pages +inf, pages past the end -inf.  Two
+    launches; the per-head logits go through a persistent workspace."""
+    _check_index_inputs(q, kmin, kmax, block_tables, seq_lens)
+    if page != PAGE:
+        raise ValueError(f"the HIP indexer reads {PAGE}-token pages")
+    b, h, n_rep, d = q.shape
+    max_pages = block_tables.shape[1]
+    scores = _score_buffer(b, h, max_pages, q.device)
+    nbytes = _lib.lib().ls_page_mass_workspace_bytes(b, h, n_rep, max_pages)
+    work = scratch("sparse_mass_heads", (max(1, nbytes // 4),), torch.float32, q.device)
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
+    P, S = _lib.ptr, _lib.strides
+    rc = _lib.lib().ls_page_scores_mass(
+        P(q), S(q, 3), P(kmin), P(kmax), S(kmin, 2), kmin.shape[0], P(block_tables),
+        block_tables.stride(0), max_pages, P(seq_lens), P(work), P(scores), S(scores, 2),
+        b, h, n_rep, d, PAGE, int(recent), float(scale), _lib.stream_of(q.device))
+    _lib.check(rc, "ls_page_scores_mass")
+    return scores
+
+
 def select(scores: torch.Tensor, k: int, sorted: bool = False,
            seq_lens: Optional[torch.Tensor] = None, ratio: Optional[float] = None,
            recent: int = 2) -> torch.Tensor:
@@ -232,15 +257,18 @@ def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
     context) when given, else the table's width; each sequence then attends
     its own budget for its current length.  Two launches (the decode
     selects), or three with ``fused=False``."""
-    if scoring != "bounds":
-        raise ValueError(f"scoring {scoring!r} is not provided by the HIP backend "
-                         "(only 'bounds')")
+    if scoring not in ("bounds", "mass"):
+        raise ValueError(f"unknown scoring {scoring!r} (bounds or mass)")
     page = k_pool.shape[1]
     pages = block_tables.shape[1] if max_seq_len is None else min(
         block_tables.shape[1], -(-int(max_seq_len) // page))
     k = budget(ratio, pages, recent)
     if not fused:
-        sel = index_select(q, kmin, kmax, block_tables, seq_lens, k, ratio, recent)
+        if scoring == "mass":
+            mass = page_scores_mass(q, kmin, kmax, block_tables, seq_lens, recent, softmax_scale)
+            sel = select(mass, k, seq_lens=seq_lens, ratio=ratio, recent=recent)
+        else:
+            sel = index_select(q, kmin, kmax, block_tables, seq_lens, k, ratio, recent)
         return sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel, num_splits,
                              softmax_scale, ratio=ratio, recent=recent, out=out)
     reason = pdh.ineligible_reason(q, k_pool)
@@ -252,7 +280,10 @@ def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
     if block_tables.shape[1] > SELECT_MAX_PAGES:
         raise ValueError(f"selection supports up to {SELECT_MAX_PAGES} pages, "
                          f"got {block_tables.shape[1]}")
-    scores = page_scores(q, kmin, kmax, block_tables, seq_lens, recent)
+    if scoring == "mass":
+        scores = page_scores_mass(q, kmin, kmax, block_tables, seq_lens, recent, softmax_scale)
+    else:
+        scores = page_scores(q, kmin, kmax, block_tables, seq_lens, recent)
     b, h, n_rep, d = q.shape
     splits = num_splits or pdh.choose_splits(b, h, k, q.device)
     splits = max(1, min(splits, max(1, k), pdh.MAX_SPLITS))

@@ -110,6 +110,7 @@ class _Attn:
     def __init__(self):
         self.num_splits: Optional[int] = None
         self.sparse_recent = 2
+        self.sparse_scoring = "bounds"
 
 
 class _Layer:
@@ -185,8 +186,11 @@ class QwenDecoder:
         self.rope = Rope(self.cfg.head_dim, self.cfg.rope_theta, max_seq_len, self.device)
         return self.cache
 
-    def set_sparse(self, ratio: Optional[float], recent: int = 2) -> None:
-        """Sparse decode attention over a page budget (None: dense)."""
+    def set_sparse(self, ratio: Optional[float], recent: int = 2,
+                   scoring: Optional[str] = None) -> None:
+        """Sparse decode attention over a page budget (None: dense), pages
+        ranked by their Quest bound ("bounds") or summed estimated mass
+        ("mass"; unchanged when None)."""
         if ratio is not None:
             if isinstance(self.cache, Int8PagedKVCache):
                 raise ValueError("sparse decode reads fp16 pools; this cache is INT8")
@@ -194,6 +198,8 @@ class QwenDecoder:
         self.sparse_ratio = ratio
         for layer in self.layers:
             layer.attn.sparse_recent = recent
+            if scoring is not None:
+                layer.attn.sparse_scoring = scoring
 
     @torch.no_grad()
     def decode_forward_static(self, token_ids: torch.Tensor, positions: torch.Tensor,
@@ -273,7 +279,8 @@ class QwenDecoder:
                 ps.sparse_attention(q, cache.k_pool[li], cache.v_pool[li], tables, lens, kmin,
                                     kmax, ratio=self.sparse_ratio,
                                     recent=layer.attn.sparse_recent, max_seq_len=ctx,
-                                    softmax_scale=self.scale, out=o)
+                                    softmax_scale=self.scale, out=o,
+                                    scoring=layer.attn.sparse_scoring)
             x = _linear(o.view(b, hq * hd), layer.w_o, layer.p_o)
             # (the gate/up projection keeps its norm launch: over its 1120
             # workgroups the prologue costs more than the launch it saves)

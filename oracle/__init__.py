@@ -23,6 +23,11 @@ How each function is pinned (tests/test_oracle.py):
   error bound |x - q*s| <= s/2 and the all-zero block.
 * ``page_scores`` — brute-force Quest bound from per-page min/max computed by
   numpy over the gathered K; forced pages are the sets {0, P-recent..P-1}.
+* ``page_scores_mass`` — an fp64 numpy brute force from the same bounds
+  (per-head softmax over the pages of bound * scale + log(count), summed),
+  a closed form (one live page below the forced ones gets all the mass of
+  every head: score n_rep), and the sum over the unforced live pages of
+  the unforced mass bounded by n_rep.
 * ``sparse_decode`` — brute-force attention over exactly the listed pages,
   and full-budget equality with ``paged_decode``.
 * ``combine`` — the all-empty split case and equality with one-split decode.
@@ -268,6 +273,25 @@ def page_scores(q, kmin, kmax, block_tables, seq_lens, recent: int = 2, page: in
                              _ptr(kmax), _I64(sb[0]), _I64(sb[1]), _ptr(block_tables),
                              _I64(_st(block_tables)[0]), _ptr(seq_lens), _I32(b), _I32(h),
                              _I32(nr), _I32(d), _I32(page), _I32(maxp), _I32(recent), _ptr(out))
+    return out
+
+
+def page_scores_mass(q, kmin, kmax, block_tables, seq_lens, recent: int = 2,
+                     softmax_scale=None, page: int = 16):
+    """``page_scores_mass`` (kernels/cuda/paged_sparse.py:126-161) on the CPU:
+    fp32 [B, H, max_pages] summed-mass scores."""
+    b, h, nr, d = q.shape
+    maxp = block_tables.shape[1]
+    out = np.empty((b, h, maxp), dtype=np.float32)
+    sq, sb = _st(q), _st(kmin)
+    if _st(kmax) != sb:
+        raise ValueError("kmin and kmax must share strides")
+    scale = 1.0 / math.sqrt(d) if softmax_scale is None else softmax_scale
+    lib().ls_ref_page_scores_mass(
+        _ptr(q), _I64(sq[0]), _I64(sq[1]), _I64(sq[2]), _ptr(kmin), _ptr(kmax), _I64(sb[0]),
+        _I64(sb[1]), _ptr(block_tables), _I64(_st(block_tables)[0]), _ptr(seq_lens), _I32(b),
+        _I32(h), _I32(nr), _I32(d), _I32(page), _I32(maxp), _I32(recent), _F32(scale),
+        _ptr(out))
     return out
 
 

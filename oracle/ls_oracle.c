@@ -21,6 +21,8 @@
  *   ls_ref_quantize_v      cache/int8_paged_cache.py:741-758 (write(), V part).
  *   ls_ref_page_scores     kernels/cuda/paged_sparse_fp16.cu:78-130 and
  *                          model/attention/sparse.py:57-74, 132-134.
+ *   ls_ref_page_scores_mass kernels/cuda/paged_sparse.py:126-161 and
+ *                          kernels/cuda/paged_sparse_fp16.cu:141-190.
  *   ls_ref_bounds_update   kernels/cuda/paged_sparse_fp16.cu:54-72 and
  *                          cache/paged_cache.py:452-465.
  *   ls_ref_gather          cache/paged_cache.py:486-506 and
@@ -472,6 +474,62 @@ void ls_ref_page_scores(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t s
             }
             scores[(int64_t)bh * max_pages + p] = out;
         }
+    }
+}
+
+/* Summed-mass page scores (kernels/cuda/paged_sparse.py:126-161, per-head
+ * bounds of paged_sparse_fp16.cu:141-190): for each query head r the bound
+ * b_r(p) = sum_d max(q_d lo_d, q_d hi_d), logits b_r(p) * scale + log(count
+ * of tokens in page p) (count 0, so -inf, past the end), a softmax over the
+ * row's max_pages pages (max subtracted, expf, fp32 sum in page order), the
+ * softmaxes summed over r; page 0 and the last `recent` pages +inf, pages
+ * past the end -inf.  scores fp32 [B, H, max_pages]. */
+void ls_ref_page_scores_mass(const uint16_t* q, int64_t sq_b, int64_t sq_h, int64_t sq_r,
+                             const uint16_t* kmin, const uint16_t* kmax, int64_t sb_b,
+                             int64_t sb_h, const int32_t* block_tables, int64_t sbt_b,
+                             const int32_t* seq_lens, int B, int H, int NR, int D, int PAGE,
+                             int max_pages, int recent, float scale, float* scores) {
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int bh = 0; bh < B * H; ++bh) {
+        const int b = bh / H, h = bh % H;
+        const int L = seq_lens[b];
+        const int np = (L + PAGE - 1) / PAGE;
+        float* out = scores + (int64_t)bh * max_pages;
+        float* logit = (float*)malloc(sizeof(float) * (size_t)max_pages);
+        for (int p = 0; p < max_pages; ++p) out[p] = 0.0f;
+        for (int r = 0; r < NR; ++r) {
+            const uint16_t* qr = q + (int64_t)b * sq_b + (int64_t)h * sq_h + (int64_t)r * sq_r;
+            float mx = -INFINITY;
+            for (int p = 0; p < max_pages; ++p) {
+                int cnt = L - p * PAGE;
+                cnt = cnt < 0 ? 0 : (cnt > PAGE ? PAGE : cnt);
+                if (cnt == 0) {
+                    logit[p] = -INFINITY;
+                    continue;
+                }
+                const int blk = block_tables[(int64_t)b * sbt_b + p];
+                const uint16_t* mn = kmin + (int64_t)blk * sb_b + (int64_t)h * sb_h;
+                const uint16_t* mxp = kmax + (int64_t)blk * sb_b + (int64_t)h * sb_h;
+                float s = 0.0f;
+                for (int d = 0; d < D; ++d) {
+                    const float qd = h2f(qr[d]);
+                    const float x = qd * h2f(mn[d]), y = qd * h2f(mxp[d]);
+                    s += x > y ? x : y;
+                }
+                const float bs = s * scale;
+                logit[p] = bs + logf((float)cnt);
+                if (logit[p] > mx) mx = logit[p];
+            }
+            if (mx == -INFINITY) continue;
+            float sum = 0.0f;
+            for (int p = 0; p < max_pages; ++p) sum += expf(logit[p] - mx);
+            for (int p = 0; p < max_pages; ++p) out[p] += expf(logit[p] - mx) / sum;
+        }
+        for (int p = 0; p < max_pages; ++p) {
+            if (p >= np) out[p] = -INFINITY;
+            else if (p == 0 || p >= np - recent) out[p] = INFINITY;
+        }
+        free(logit);
     }
 }
 

@@ -182,6 +182,45 @@ def test_gpu_selection_agrees_with_the_oracle_selection():
     sets_agree(g, w, scores, None)
 
 
+# ------------------------------------------------------- mass scoring ----
+@pytest.mark.parametrize("n_rep,recent", [(6, 2), (1, 0), (16, 3)])
+def test_page_scores_mass_match_the_oracle(n_rep, recent):
+    width = 300
+    lens = [width * 16, 2500, 700, 40, 1, 0]
+    q, k, v, t, l, kmin, kmax = index_case(lens, width=width, n_rep=n_rep, seed=n_rep)
+    Q, T, L, KN, KX = dev(q, t, l, kmin, kmax)
+    got = ps().page_scores_mass(Q, KN, KX, T, L, recent=recent).cpu().numpy()
+    want = oracle.page_scores_mass(q, kmin, kmax, t, l, recent=recent)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[~fin], want[~fin])
+    assert_close(got[fin], want[fin], 1e-7, 1e-4, f"mass n_rep={n_rep}")
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_sparse_attention_mass_scoring(fused):
+    """scoring="mass" (kernels/cuda/paged_sparse.py:236-237): the pages the
+    GPU keeps agree with the oracle's top-k of the oracle's mass scores, and
+    the output is the oracle's attention over the GPU's pages."""
+    width = 256
+    lens = [width * 16, 2500, 700, 40]
+    q, k, v, t, l, kmin, kmax = index_case(lens, width=width, seed=11)
+    Q, K, V, T, L, KN, KX = dev(q, k, v, t, l, kmin, kmax)
+    out = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=0.25, scoring="mass",
+                                fused=fused).float().cpu().numpy()
+    kk = ps().budget(0.25, width)
+    mass = ps().page_scores_mass(Q, KN, KX, T, L)
+    sel = ps().select(mass, kk, seq_lens=L, ratio=0.25).cpu().numpy()
+    want_scores = oracle.page_scores_mass(q, kmin, kmax, t, l)
+    for i, length in enumerate(lens):
+        n = oracle.sparse_count(-(-length // 16), kk, 0.25)
+        want_rows = oracle.select(want_scores[i:i + 1], n)[0]
+        sets_agree([[sel[i, j, :n].tolist() for j in range(2)]],
+                   [[want_rows[j].tolist() for j in range(2)]], want_scores[i:i + 1], None,
+                   tol=1e-4)
+    want = oracle.sparse_decode(q, k, v, t, l, sel, ratio=0.25, recent=2)
+    assert_close(out, want, ATOL, RTOL, f"mass fused={fused}")
+
+
 # --------------------------------------------------- sparse attention ----
 @pytest.mark.parametrize("ratio", [0.25, 0.5, 1.0])
 def test_sparse_attention_end_to_end(ratio):

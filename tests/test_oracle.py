@@ -326,6 +326,62 @@ def test_page_scores_are_the_brute_force_quest_bound():
         assert (got[b, :, np_:] == -np.inf).all()
 
 
+def _mass_brute_force(q, kmin, kmax, t, l, recent, scale):
+    """fp64: per query head, softmax over the live pages of bound * scale +
+    log(tokens in the page); summed over the heads; forced / past-end
+    overrides (kernels/cuda/paged_sparse.py:126-161)."""
+    b_, h_, nr, d = q.shape
+    maxp = t.shape[1]
+    out = np.zeros((b_, h_, maxp))
+    for b in range(b_):
+        L = int(l[b])
+        np_ = -(-L // 16)
+        cnt = np.clip(L - np.arange(np_) * 16, 0, 16).astype(np.float64)
+        lo = kmin[t[b, :np_]].astype(np.float64)                     # [P, H, D]
+        hi = kmax[t[b, :np_]].astype(np.float64)
+        for h in range(h_):
+            qf = q[b, h].astype(np.float64)                          # [NR, D]
+            bound = np.maximum(qf[:, None, :] * lo[None, :, h], qf[:, None, :] * hi[None, :, h]).sum(-1)
+            logit = bound * scale + np.log(cnt)[None]
+            w = np.exp(logit - logit.max(axis=1, keepdims=True))
+            out[b, h, :np_] = (w / w.sum(axis=1, keepdims=True)).sum(0)
+            out[b, h, np_:] = -np.inf
+            out[b, h, 0] = np.inf
+            if recent:
+                out[b, h, max(0, np_ - recent):np_] = np.inf
+    return out
+
+
+@pytest.mark.parametrize("recent", [2, 0])
+def test_page_scores_mass_is_the_brute_force_softmax_sum(recent):
+    q, k, v, t, l = paged_case([700, 333, 16, 1], seed=4, extra_blocks=3)
+    kmin, kmax = _bounds_from_pool(k)
+    scale = 1.0 / math.sqrt(128)
+    got = oracle.page_scores_mass(q, kmin, kmax, t, l, recent=recent)
+    want = _mass_brute_force(q, kmin, kmax, t, l, recent, scale)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[~fin], want[~fin])
+    assert_close(got[fin], want[fin], 1e-7, 1e-5, "mass scores")
+    # the unforced mass of a row never exceeds the n_rep heads' total
+    assert (np.where(fin, got, 0).sum(-1) <= 6 + 1e-5).all()
+
+
+def test_page_scores_mass_one_dominant_page_takes_every_head():
+    """Every query row positive, every page's K bounds -1 except page 5's
+    +10: page 5 takes (to fp32) all of each head's softmax, score = n_rep."""
+    q = np.ones((1, 2, 6, 128), np.float16)
+    nb = 12
+    kmin = np.full((nb, 2, 128), -1, np.float16)
+    kmax = kmin.copy()
+    t = np.arange(10, dtype=np.int32)[None]
+    kmin[5] = kmax[5] = 10
+    l = np.array([160], np.int32)
+    got = oracle.page_scores_mass(q, kmin, kmax, t, l, recent=2)
+    assert np.allclose(got[0, :, 5], 6.0, rtol=0, atol=1e-6)
+    others = [p for p in range(1, 8) if p != 5]
+    assert (got[0][:, others] < 1e-30).all()
+
+
 def test_bounds_update_tracks_running_min_max():
     rng = np.random.default_rng(1)
     nb, h, d = 8, 2, 16
