@@ -98,4 +98,55 @@ __device__ __forceinline__ _Float16 rope_h(_Float16 x, _Float16 c, _Float16 y, _
     return (_Float16)((float)xc + (float)ys);
 }
 
+// Hand-off of partial results between the workgroups of one launch: many
+// groups write their partials, then bump an arrival counter (a relaxed
+// agent-scope RMW); the group that brings the count to its target reads
+// them all.
+//
+// Release side: the partials are stored write-through at device coherence
+// (sc1: the line is written to memory, not held dirty in this XCD's L2) and
+// handoff_release() waits for those stores to complete before the RMW is
+// issued.  This is the release the partials need, stated at the ISA level:
+// the HIP model's agent-scope release fence would add a write-back of the
+// whole L2 (buffer_wbl2) in every wave, measured at +16 us a launch on the
+// B16 x 16K decode (49.6 -> 65.5 us).  Only stores made write-through may
+// be handed off this way.
+// Acquire side: the last arriver reads the partials with device-coherent
+// loads (sc1, relaxed agent-scope atomic loads), issued after its RMW has
+// returned the final count (the branch on it orders them), so no line can
+// come from a stale copy in its XCD's L2.  The model's agent-scope acquire
+// fence (an invalidate of the reader's whole L2) measured +2.1 us a launch
+// on the same decode; these loads +0.65 us (49.5 -> 50.2 us), over the
+// plain loads an earlier form used, which were right only while the
+// reader's L2 held no copy of the partials' lines.
+// Device-coherent loads (sc1: served from memory or a coherent copy, never
+// from a stale line in this XCD's L2), as relaxed agent-scope atomic loads.
+template <class T>
+__device__ __forceinline__ T load_coherent(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sixteen bytes the same way (a global_load_dwordx4 with sc1).  The
+// compiler does not track an asm load: the caller issues its loads, then
+// coherent_wait() on every value loaded before using any of them.
+__device__ __forceinline__ f4 load_coherent4_issue(const float* p) {
+    f4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+__device__ __forceinline__ void coherent_wait() {
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+}
+// Ties a value to the wait above it: later uses read the register after it.
+template <class T>
+__device__ __forceinline__ void coherent_pin(T& v) {
+    asm volatile("" : "+v"(v));
+}
+
+__device__ __forceinline__ void handoff_release() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 }  // namespace ls

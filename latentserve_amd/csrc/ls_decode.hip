@@ -303,6 +303,8 @@ __device__ __forceinline__ void store_coherent4(float* p, f4 v) {
     asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
 
+// VEC 4: 16-byte loads; 1: scalar loads; 0: device-coherent scalar loads
+// (partials written by other workgroups of the same launch).
 template <int VEC>
 __device__ void combine_partials(const float* acc, const float* m, const float* l, int S, int NR,
                                  int64_t sa_s, int64_t sa_r, int64_t sm_s, void* out, int out_f32,
@@ -314,15 +316,22 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
         for (int s0 = 0; s0 < S; s0 += CMB_CHUNK) {
             const int n = S - s0 < CMB_CHUNK ? S - s0 : CMB_CHUNK;
             float mv[CMB_CHUNK], lv[CMB_CHUNK], av[CMB_CHUNK][4];
+            f4 avc[CMB_CHUNK];
             // Every slot loads (slots past the last split reread it) and is
             // masked afterwards: loads under a branch would each wait for
             // the one before.
 #pragma unroll
             for (int i = 0; i < CMB_CHUNK; ++i) {
                 const int64_t sp = s0 + i < S ? s0 + i : S - 1;
+                const float* src = acc + sp * sa_s + r * sa_r + d0;
+                if (VEC == 0) {
+                    mv[i] = load_coherent(m + sp * sm_s + r);
+                    lv[i] = load_coherent(l + sp * sm_s + r);
+                    avc[i] = load_coherent4_issue(src);
+                    continue;
+                }
                 mv[i] = m[sp * sm_s + r];
                 lv[i] = l[sp * sm_s + r];
-                const float* src = acc + sp * sa_s + r * sa_r + d0;
                 if (VEC == 4) {
                     const f4 t = *(const f4*)src;
 #pragma unroll
@@ -330,6 +339,15 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) av[i][e] = src[e];
+                }
+            }
+            if (VEC == 0) {
+                coherent_wait();
+#pragma unroll
+                for (int i = 0; i < CMB_CHUNK; ++i) {
+                    coherent_pin(avc[i]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) av[i][e] = avc[i][e];
                 }
             }
 #pragma unroll
@@ -1051,12 +1069,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     if (single) return;
 
     // ---- the last group of each (b, h) to arrive merges all splits ----
-    // The records above bypass the non-coherent L2 path, so ordering needs
-    // only their completion before the arrival count: no whole-L2 writeback
-    // or invalidate (which a device-scope fence would issue in every group).
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // Every wave's write-through record stores complete before the group's
+    // arrival; the last arriver acquires before reading them.
+    handoff_release();
     __syncthreads();
     if (threadIdx.x < (unsigned)HG) {
         const int64_t bh = (int64_t)b * H + h0 + threadIdx.x;
@@ -1070,10 +1085,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     if (!sm.is_last[hh]) return;
     const int64_t bh = (int64_t)b * H + h0 + hh;
     {
-        // The records were written through to memory and no group has read
-        // their lines in this launch, so plain vector loads see them.
+        // device-coherent loads: the records of groups on other XCDs
         const float* recs = a.work + ((int64_t)gw.first * H + h0 + hh) * rec;
-        combine_partials<4>(recs, recs + NR * HEAD_DIM, recs + NR * HEAD_DIM + MAX_NREP, Sb, NR,
+        combine_partials<0>(recs, recs + NR * HEAD_DIM, recs + NR * HEAD_DIM + MAX_NREP, Sb, NR,
                             (int64_t)H * rec, HEAD_DIM, (int64_t)H * rec,
                             a.out + (int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h, 0, a.so_r,
                             t256);

@@ -344,16 +344,15 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_rows_kernel(ArgmaxParam
     if (threadIdx.x == 0) {
         store_through(a.part_v + (int64_t)row * a.parts + part, bv);
         store_through(a.part_i + (int64_t)row * a.parts + part, bi);
-        __builtin_amdgcn_s_waitcnt(0);
+        handoff_release();
         last = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT) == (unsigned)a.parts - 1;
     }
     __syncthreads();
     if (!last || threadIdx.x != 0) return;
-    // the parts were written through and not read before in this launch
-    for (int p = 0; p < a.parts; ++p) {
-        const float v = a.part_v[(int64_t)row * a.parts + p];
-        const int i = a.part_i[(int64_t)row * a.parts + p];
+    for (int p = 0; p < a.parts; ++p) {                // device-coherent loads
+        const float v = load_coherent(a.part_v + (int64_t)row * a.parts + p);
+        const int i = load_coherent(a.part_i + (int64_t)row * a.parts + p);
         if (p == 0 || argmax_better(v, i, bv, bi)) {
             bv = v;
             bi = i;

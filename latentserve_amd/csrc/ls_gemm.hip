@@ -538,29 +538,26 @@ __global__ __launch_bounds__(256) void decode_gemm_kernel(GemmParams a) {
                 store_through4(a.part + ((int64_t)blockIdx.y * a.M + m) * ldp + nc, acc[t][mb]);
         }
     }
-    // The partials bypass the non-coherent L2 path, so ordering needs only
-    // their completion before the arrival count (no whole-L2 writeback or
-    // invalidate, which a device-scope fence would issue).
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // the write-through partials complete before the arrival count
+    handoff_release();
     int prev = 0;
     if (lane == 0)
         prev = __hip_atomic_fetch_add(a.counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
     prev = __shfl(prev, 0);
     if (prev != a.splits - 1) return;
-    // Every split of these tiles has arrived.  Their partials were written
-    // through to memory and no group has read those lines in this launch,
-    // so plain loads see them.  Unit u = (t, m, q): four columns.
+    // Every split of these tiles has arrived; their partials are read with
+    // device-coherent loads.  Unit u = (t, m, q): four columns.
     const int64_t split_stride = (int64_t)a.M * ldp;
     for (int u = lane; u < TPW * a.M * 4; u += WAVE) {
         const int t = u / (a.M * 4), m = (u / 4) % a.M, q = u % 4;
         const int nc = 16 * (tile0 + t) + 4 * q;
         if (nc >= a.N) continue;
         const float* pp = a.part + (int64_t)m * ldp + nc;
-        f4 s = *(const f4*)pp;
-        for (int sp = 1; sp < a.splits; ++sp) s += *(const f4*)(pp + sp * split_stride);
+        f4 s = {0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < a.splits; ++sp)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[e] += load_coherent(pp + sp * split_stride + e);
         half_t o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
