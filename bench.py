@@ -69,6 +69,13 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seqs", type=int, default=None,
                    help="sequences in the CPU-baseline sample (default: the whole batch)")
+    p.add_argument("--compute-probe", type=int, default=0, metavar="ITEMS",
+                   help="instead of the benchmark, time the decode kernel's page compute alone "
+                        "(MFMA, as built) against a VALU formulation, ITEMS pages a wave, from "
+                        "the measurement build given by --diag-lib, and exit")
+    p.add_argument("--diag-lib", default=None, metavar="PATH",
+                   help="the -DLS_DIAGNOSTICS build (python -m latentserve_amd.csrc.build "
+                        "--diagnostics PATH) that holds the page-compute probe")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="instead of the benchmark, run device copies of MIB MiB (for the "
                         "rocprof FETCH_SIZE / WRITE_SIZE scale factor) and exit")
@@ -268,6 +275,51 @@ def calibrate_copy(mib):
     print(json.dumps({"calibrate_copy_bytes": n, "launches": 5}))
 
 
+def compute_probe(items, diag_lib):
+    """The page compute from registers, 8 waves a CU as the decode kernel
+    runs: one page's QK, softmax and PV per wave, MFMA (mode 0) against VALU
+    (mode 1), from the measurement build's ls_compute_probe.  Every wave
+    applies one synthetic page (16 tokens, 6 rows, 128 channels, values
+    exact in fp16) `items` times, so its output equals the page's fp32
+    attention whatever `items` is."""
+    import ctypes
+
+    import torch
+    if not diag_lib:
+        sys.exit("--compute-probe needs --diag-lib PATH (the -DLS_DIAGNOSTICS build)")
+    lib = ctypes.CDLL(diag_lib)
+    fn = lib.ls_compute_probe
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_void_p,
+                   ctypes.c_void_p]
+    t = torch.arange(16).view(-1, 1)
+    r = torch.arange(6).view(-1, 1)
+    ch = torch.arange(128).view(1, -1)
+    k = ((t * 7 + ch * 3) % 17 - 8).float() * 0.0625
+    v = ((t * 5 + ch * 11) % 13 - 6).float() * 0.125
+    q = ((r * 13 + ch * 5) % 11 - 5).float() * 0.125
+    scale = 1.0 / math.sqrt(128)
+    want = (torch.softmax((q @ k.t()) * scale, dim=-1) @ v).cuda()
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {"items_per_wave": items}
+    for groups in (256, 512):
+        for mode, name in ((0, "mfma"), (1, "valu")):
+            out = torch.empty(groups * 8, 6, 128, dtype=torch.float32, device="cuda")
+            assert fn(mode, groups, 8, scale, out.data_ptr(), stream) == 0
+            torch.cuda.synchronize()
+            err = (out - want).abs().max().item()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(5):
+                assert fn(mode, groups, items, scale, out.data_ptr(), stream) == 0
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / 5
+            res[f"{name}_g{groups}"] = {"us": round(us, 2),
+                                        "ns_per_page_per_wave": round(us * 1e3 / items, 2),
+                                        "max_abs_err": err}
+    print(json.dumps(res))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -279,6 +331,9 @@ def main():
 
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
+        return
+    if args.compute_probe:
+        compute_probe(args.compute_probe, args.diag_lib)
         return
     cfg = CONFIGS[args.config]
     if cfg["kind"] == "step":
