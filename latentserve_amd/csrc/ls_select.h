@@ -47,6 +47,7 @@ struct SelectSmem {
     uint32_t hist[2][2][256];          // [pass parity][threshold][digit]
     uint32_t wsum[2][4];               // [scan parity][wave]
     int found[4];
+    uint32_t pfx[2][4];                // [and, or][wave]
 };
 
 // Inclusive prefix sum over the 256 threads of a group (tid: the thread's
@@ -108,8 +109,65 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
     int nscan = 0;
     sm.hist[0][0][tid] = 0;
     sm.hist[0][1][tid] = 0;
-    __syncthreads();
-    for (int shift = 24, par = 0; shift >= 0; shift -= 8, par ^= 1) {
+    // The finite scores of a row share their leading bits (one exponent):
+    // a pass over them would put every key in one bin.  So the bits common
+    // to the finite keys (forced pages +inf and pages past the end -inf
+    // excluded) are found first, and when both thresholds fall among the
+    // keys with that prefix, the passes start right below it.
+    int shift = 24;
+    {
+        constexpr uint32_t KEY_PINF = 0xFF800000u, KEY_NINF = 0x007FFFFFu;
+        uint32_t kand = 0xFFFFFFFFu, kor = 0u;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            if (j < cnt && key[j] != KEY_PINF && key[j] != KEY_NINF) {
+                kand &= key[j];
+                kor |= key[j];
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            kand &= (uint32_t)__shfl_xor((int)kand, o);
+            kor |= (uint32_t)__shfl_xor((int)kor, o);
+        }
+        if ((tid & 63) == 0) {
+            sm.pfx[0][tid >> 6] = kand;
+            sm.pfx[1][tid >> 6] = kor;
+        }
+        __syncthreads();
+        kand = sm.pfx[0][0] & sm.pfx[0][1] & sm.pfx[0][2] & sm.pfx[0][3];
+        kor = sm.pfx[1][0] | sm.pfx[1][1] | sm.pfx[1][2] | sm.pfx[1][3];
+        const bool any = kand <= kor;                    // some finite key
+        const uint32_t diff = kand ^ kor;
+        const int h = diff ? 31 - __builtin_clz(diff) : 0;   // highest differing bit
+        const uint32_t hi = h >= 31 ? 0u : ~((2u << h) - 1u); // the common bits
+        const uint32_t p0 = kand & hi;
+        uint32_t above = 0, same = 0;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            if (j < cnt) {
+                above += (key[j] & hi) > p0 ? 1u : 0u;
+                same += (key[j] & hi) == p0 ? 1u : 0u;
+            }
+        }
+        const int par = nscan++ & 1;
+        (void)group_scan(above | (same << 16), sm.wsum[par], tid);
+        const uint32_t tot = sm.wsum[par][0] + sm.wsum[par][1] + sm.wsum[par][2] + sm.wsum[par][3];
+        const int A = (int)(tot & 0xFFFFu), M = (int)(tot >> 16);
+        auto inside = [&](int n) { return n == 0 || (A < n && n <= A + M); };
+        if (any && hi != 0u && inside(n1) && inside(n2)) {
+            pre0 = pre1 = p0;
+            msk = hi;
+            rem0 = n1 > 0 ? n1 - A : 0;
+            rem1 = n2 > 0 ? n2 - A : 0;
+            shift = h - 7;
+        }
+    }
+    for (int par = 0;; par ^= 1) {
+        // (a pass below bit 0 repeats the bits of the last: the keys that
+        // still match the prefix agree on them, so such a pass changes
+        // nothing; it runs only while another group of the workgroup goes on)
+        const int sh = shift > 0 ? shift : 0;
         // A thread's keys are adjacent pages whose leading digits mostly
         // agree (one exponent for the whole row): count runs of equal digits
         // and add each run once, instead of one LDS atomic per key on a
@@ -118,7 +176,7 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
             if (j < cnt) {
-                const uint32_t d = (key[j] >> shift) & 255u;
+                const uint32_t d = (key[j] >> sh) & 255u;
                 if ((key[j] & msk) == pre0) {
                     if (d != d0) {
                         if (n0) atomicAdd(&sm.hist[par][0][d0], n0);
@@ -163,17 +221,19 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
             open = open || rem1 - ce1 != ci1 - ce1;
         }
         // the whole workgroup goes on while any of its groups has a side open
-        const bool more = __syncthreads_or(open);
+        // (after the pass at bit 0 every bit is decided: nothing is open)
+        const bool more = __syncthreads_or(open && sh > 0);
         if (rem0 > 0) {
-            pre0 |= (uint32_t)sm.found[0] << shift;
+            pre0 |= (uint32_t)sm.found[0] << sh;
             rem0 = sm.found[1];
         }
         if (rem1 > 0) {
-            pre1 |= (uint32_t)sm.found[2] << shift;
+            pre1 |= (uint32_t)sm.found[2] << sh;
             rem1 = sm.found[3];
         }
-        msk |= 255u << shift;
+        msk |= 255u << sh;
         if (!more) break;
+        shift -= 8;
     }
     // threshold prefixes pre0 / pre1 of the keys under msk; rem0 / rem1 =
     // how many keys with that prefix belong to the set (the lowest pages
