@@ -186,6 +186,35 @@ int ls_page_scores(const void* q, const int64_t* q_strides, const void* kmin, co
                    const int64_t* score_strides, int batch, int kv_heads, int n_rep, int head_dim,
                    int page, int recent, void* stream);
 
+/* sparse_attention with bounds scoring in ONE launch: the page scores are
+ * computed by the decode's own workgroups (each scores its share of its
+ * sequence's pages, Quest bound of kmin/kmax fp16 [num_blocks, H_kv, 128],
+ * bound_strides (block, head); page 0 and the last `recent` pages +inf,
+ * pages past the end -inf), exchanged through `scores` fp32 [B, H_kv,
+ * >= max_pages + 1] (the word after a row counts the workgroups that have
+ * stored their share; every byte 0xFF before the first call, and every call
+ * leaves it so), then each workgroup selects and attends as
+ * ls_sparse_attention_fp16 does.  A share that has not arrived after 50 us
+ * is computed by the reader itself, so no workgroup depends on another
+ * being resident.
+ * Replaces the index + select + attend steps of sparse_attention
+ * (kernels/cuda/paged_sparse.py:222-251; page_index, paged_sparse_fp16.cu:
+ * 78-130).  k <= max_pages <= 2048 (COOP_MAX_PAGES), n_rep <= 8
+ * (COOP_MAX_NREP), ceil(k / num_splits) <= 1024; longer rows or more query
+ * rows a KV head take ls_page_scores + ls_sparse_attention_fp16. */
+int ls_sparse_attention_bounds_fp16(const void* q, const int64_t* q_strides,
+                                    const void* k_pool, const void* v_pool,
+                                    const int64_t* kv_strides, int num_blocks,
+                                    const int32_t* block_tables, int64_t bt_stride,
+                                    int max_pages, const int32_t* seq_lens, const void* kmin,
+                                    const void* kmax, const int64_t* bound_strides,
+                                    float* scores, const int64_t* score_strides, int k,
+                                    float ratio, int recent, void* out,
+                                    const int64_t* out_strides, float* workspace,
+                                    int32_t* counters, int batch, int kv_heads, int n_rep,
+                                    int head_dim, int page, int num_splits, int max_seq_len,
+                                    float softmax_scale, void* stream);
+
 /* Bytes of `workspace` ls_page_scores_mass needs: the per-head logits,
  * fp32 [batch, kv_heads, n_rep, max_pages]. */
 size_t ls_page_mass_workspace_bytes(int batch, int kv_heads, int n_rep, int max_pages);

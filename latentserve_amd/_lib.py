@@ -28,7 +28,7 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -45,6 +45,10 @@ _SIGNATURES = {
     "ls_page_scores_mass": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _VP, _I64P, _I32, _I32,
         _I32, _I32, _I32, _I32, _F32, _VP],
+    "ls_sparse_attention_bounds_fp16": [
+        _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _VP, _I64P, _VP, _I64P,
+        _I32, _F32, _I32, _VP, _I64P, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
+        _VP],
     "ls_paged_decode_int8": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64P, _VP, _I64P, _VP, _VP,
         _VP, _I64P, _I32, _VP, _VP, _I64, _I32, _VP, _VP, _I64P,

@@ -229,7 +229,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 15; }
+int ls_abi_version(void) { return 16; }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -406,7 +406,7 @@ int ls_sparse_attention_fp16(const void* q, const int64_t* q_strides, const void
                 max_pages, seq_lens, out, out_strides, workspace, counters, batch,
                 kv_heads, n_rep, num_splits, max_seq_len, softmax_scale);
     a.kind = ls::KV_FP16;
-    a.scores = scores;
+    a.scores = const_cast<float*>(scores);
     a.ssc_b = score_strides[0];
     a.ssc_h = score_strides[1];
     a.score_pages = score_pages;
@@ -414,6 +414,62 @@ int ls_sparse_attention_fp16(const void* q, const int64_t* q_strides, const void
     a.ratio = ratio;
     a.recent = recent;
     return hip_status(ls::launch_decode(a, (hipStream_t)stream), "ls_sparse_attention_fp16");
+}
+
+int ls_sparse_attention_bounds_fp16(const void* q, const int64_t* q_strides,
+                                    const void* k_pool, const void* v_pool,
+                                    const int64_t* kv_strides, int num_blocks,
+                                    const int32_t* block_tables, int64_t bt_stride,
+                                    int max_pages, const int32_t* seq_lens, const void* kmin,
+                                    const void* kmax, const int64_t* bound_strides,
+                                    float* scores, const int64_t* score_strides, int k,
+                                    float ratio, int recent, void* out,
+                                    const int64_t* out_strides, float* workspace,
+                                    int32_t* counters, int batch, int kv_heads, int n_rep,
+                                    int head_dim, int page, int num_splits, int max_seq_len,
+                                    float softmax_scale, void* stream) {
+    if (!kmin || !kmax || !bound_strides) return fail(LS_ERR_INVALID, "needs kmin, kmax");
+    if (!rows_aligned(kmin, bound_strides, 2, 2, 16) || !rows_aligned(kmax, bound_strides, 2, 2, 16))
+        return fail(LS_ERR_INVALID, "kmin/kmax rows must be 16-byte aligned");
+    if (recent < 0) return fail(LS_ERR_INVALID, "recent must be >= 0");
+    if (!aligned(scores, 4)) return fail(LS_ERR_INVALID, "scores must be 4-byte aligned");
+    int rc = check_common(q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables,
+                          max_pages, seq_lens, out, out_strides, workspace,
+                          counters, batch, kv_heads, n_rep, head_dim, page, num_splits, 2);
+    if (rc) return rc;
+    if (!scores || !score_strides) return fail(LS_ERR_INVALID, "needs the score buffer");
+    if (score_strides[1] < (int64_t)max_pages + 1 || score_strides[0] < kv_heads * score_strides[1])
+        return fail(LS_ERR_INVALID, "score rows need max_pages + 1 words (a count after each)");
+    if (max_pages > ls::COOP_MAX_PAGES)
+        return fail(LS_ERR_INVALID, "max_pages must be at most %d, got %d",
+                    ls::COOP_MAX_PAGES, max_pages);
+    if (n_rep > ls::COOP_MAX_NREP)
+        return fail(LS_ERR_INVALID, "n_rep must be at most %d, got %d", ls::COOP_MAX_NREP, n_rep);
+    if (k < 0 || k > max_pages)
+        return fail(LS_ERR_INVALID, "k must be in [0, max_pages], got %d", k);
+    if ((k + num_splits - 1) / num_splits > ls::SELECT_SPLIT_ENTRIES)
+        return fail(LS_ERR_INVALID,
+                    "k / num_splits must be at most %d (k %d, num_splits %d): use more splits",
+                    ls::SELECT_SPLIT_ENTRIES, k, num_splits);
+    if (batch == 0) return LS_OK;
+    ls::DecodeParams a;
+    fill_common(a, q, q_strides, k_pool, v_pool, kv_strides, num_blocks, block_tables, bt_stride,
+                max_pages, seq_lens, out, out_strides, workspace, counters, batch,
+                kv_heads, n_rep, num_splits, max_seq_len, softmax_scale);
+    a.kind = ls::KV_FP16;
+    a.scores = scores;
+    a.ssc_b = score_strides[0];
+    a.ssc_h = score_strides[1];
+    a.score_pages = max_pages;
+    a.kmin = kmin;
+    a.kmax = kmax;
+    a.sb_b = bound_strides[0];
+    a.sb_h = bound_strides[1];
+    a.num_sel = k;
+    a.ratio = ratio;
+    a.recent = recent;
+    return hip_status(ls::launch_decode(a, (hipStream_t)stream),
+                      "ls_sparse_attention_bounds_fp16");
 }
 
 int ls_combine_splits(const float* part_acc, const int64_t* acc_strides, const float* part_m,
@@ -505,7 +561,7 @@ int ls_page_scores_mass(const void* q, const int64_t* q_strides, const void* kmi
     a.sbt_b = bt_stride;
     a.max_pages = max_pages;
     a.seq_lens = seq_lens;
-    a.scores = scores;
+    a.scores = const_cast<float*>(scores);
     a.ss_b = score_strides[0];
     a.ss_h = score_strides[1];
     a.B = batch;
@@ -567,7 +623,7 @@ int ls_sparse_index(const void* q, const int64_t* q_strides, const void* kmin, c
     a.sbt_b = bt_stride;
     a.max_pages = max_pages;
     a.seq_lens = seq_lens;
-    a.scores = scores;
+    a.scores = const_cast<float*>(scores);
     a.ss_b = score_strides[0];
     a.ss_h = score_strides[1];
     a.B = batch;
@@ -612,7 +668,7 @@ int ls_page_select(const float* scores, const int64_t* score_strides, const int3
         return fail(LS_ERR_INVALID, "k must be in [0, num_pages=%d], got %d", num_pages, k);
     if (batch == 0 || k == 0) return LS_OK;
     ls::SelectParams a;
-    a.scores = scores;
+    a.scores = const_cast<float*>(scores);
     a.ss_b = score_strides[0];
     a.ss_h = score_strides[1];
     a.seq_lens = seq_lens;
@@ -1154,7 +1210,7 @@ int ls_pack_gemm_weight(const void* w, int64_t w_stride, int N, int K, int kind,
     if (kind < 0 || kind > 2) return fail(LS_ERR_INVALID, "kind must be 0, 1 or 2, got %d", kind);
     if (kind == 1 && N % 2 != 0) return fail(LS_ERR_INVALID, "a gate/up weight has 2I rows");
     if (kind == 2 && (head_dim < 16 || head_dim % 16 != 0 || N % head_dim != 0))
-        return fail(LS_ERR_INVALID, "a q/k/v weight needs head_dim % 16 == 0 dividing N");
+        return fail(LS_ERR_INVALID, "a q/k/v weight needs head_dim %% 16 == 0 dividing N");
     if (!aligned(w, 16) || w_stride % 8 != 0 || w_stride < K || !aligned(packed, 16))
         return fail(LS_ERR_INVALID, "w rows and packed must be 16-byte aligned");
     return hip_status(ls::launch_pack_gemm_weight(w, w_stride, N, K, kind, head_dim, packed,

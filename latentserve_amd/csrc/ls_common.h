@@ -24,6 +24,10 @@ constexpr int MAX_NREP = 16;    // query rows per KV head = the N=16 side of the
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
+// A word of a buffer that other workgroups of the same launch fill: all ones
+// (a NaN payload no arithmetic here produces) until its value is stored.
+constexpr uint32_t EMPTY_WORD = 0xFFFFFFFFu;
+
 // 2^x on the transcendental unit (v_exp_f32): exact 0 for -inf.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -11,6 +11,13 @@ enum KvKind { KV_FP16 = 0, KV_INT8 = 1 };
 // List entries one group of a selecting page-subset walk keeps in its item
 // table (a split's share of the list must fit).
 constexpr int SELECT_SPLIT_ENTRIES = 1024;
+// The one-launch bounds path (each group scores a share of its sequence's
+// pages, then selects from the whole rows): rows of at most COOP_MAX_PAGES
+// pages (eight keys a thread) and at most COOP_MAX_NREP query rows a KV head
+// (their parts and sign masks stay in registers); larger shapes take the
+// index kernel and the two-launch path.
+constexpr int COOP_MAX_PAGES = 2048;
+constexpr int COOP_MAX_NREP = 8;
 
 // Everything one decode launch reads.  Strides are in elements.
 struct DecodeParams {
@@ -40,9 +47,15 @@ struct DecodeParams {
     int num_sel;
     float ratio;
     int recent;
-    const float* scores;               // non-null: page-subset walk whose list the kernel
+    float* scores;                     // non-null: page-subset walk whose list the kernel
     int64_t ssc_b, ssc_h;              // selects itself from page scores [B, H, score_pages]
     int score_pages;                   // (num_sel = the list width k)
+    // non-null with scores: the kernel computes the scores itself from the
+    // page K bounds fp16 [num_blocks, H, 128] (scores then starts all ones
+    // and is left so)
+    const void* kmin;
+    const void* kmax;
+    int64_t sb_b, sb_h;
     float* work;                       // [B * S, H] records of NR*128 + 32 floats:
                                        // acc[NR][128], m[16] (natural log), l[16]
     int pages_per_split;               // > 0: dense walk partition given by the host

@@ -50,6 +50,7 @@
 #include "ls_common.h"
 #include "ls_decode.h"
 #include "ls_select.h"
+#include "ls_quest.h"
 
 namespace ls {
 
@@ -555,8 +556,119 @@ __device__ __forceinline__ int claim_item(int* counter, int lane) {
 }
 __device__ __forceinline__ int claimed_item(int raw) { return __builtin_amdgcn_readlane(raw, 0); }
 
+// The Quest scores of the pages [p_lo, p_hi) of sequence b's rows for the
+// group's HG heads, stored write-through into a.scores (the index kernel's
+// rule: page 0 and the last `recent` pages +inf, pages past the end or with
+// a block id outside the pool -inf).  Each 16-lane row of a wave takes one
+// (page, head) unit a round, 8 channels a lane; the block ids of up to
+// four rounds are requested together, then their bounds.
+template <int NWT, int HG>
+__device__ void score_slice(const DecodeParams& a, int b, int h0, int len, int p_lo, int p_hi) {
+    const int lane = threadIdx.x % WAVE, wv = threadIdx.x / WAVE;
+    const int row = lane >> 4, c0 = (lane & 15) * 8;
+    const int np = len > 0 ? (len + PAGE - 1) / PAGE : 0;
+    constexpr int PPR = 4 / HG;                 // pages a wave takes a round
+    constexpr int R = 4;                        // rounds requested together
+    const int hh = row % HG;
+    const half_t* qb = a.q + (int64_t)b * a.sq_b + (int64_t)(h0 + hh) * a.sq_h + c0;
+    float* srow = a.scores + (int64_t)b * a.ssc_b + (int64_t)(h0 + hh) * a.ssc_h;
+    // the lane's 8 channels of every query row, loaded once, together
+    // (rows past n_rep repeat row 0 and are not used)
+    u4 qv[COOP_MAX_NREP];
+#pragma unroll
+    for (int q = 0; q < COOP_MAX_NREP; ++q) qv[q] = *(const u4*)(qb + (int64_t)(q < a.NR ? q : 0) * a.sq_r);
+    u4 qm[COOP_MAX_NREP];
+#pragma unroll
+    for (int q = 0; q < COOP_MAX_NREP; ++q) qm[q] = quest_masks(qv[q]);
+    for (int base = p_lo; base < p_hi; base += R * NWT * PPR) {
+        int pg[R], st[R];
+        int blk[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int p = base + (r * NWT + wv) * PPR + row / HG;
+            pg[r] = p;
+            st[r] = p >= p_hi ? 0 : p >= np ? 3 : (p == 0 || p >= np - a.recent) ? 2 : 1;
+            const int pc = p < a.max_pages ? p : a.max_pages - 1;
+            blk[r] = a.block_tables[(int64_t)b * a.sbt_b + pc];
+        }
+        u4 lo[R], hi[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (st[r] == 1 && (unsigned)blk[r] >= (unsigned)a.num_blocks) st[r] = 3;
+            const int bk = st[r] == 1 ? blk[r] : 0;
+            const int64_t off = (int64_t)bk * a.sb_b + (int64_t)(h0 + hh) * a.sb_h + c0;
+            lo[r] = *(const u4*)((const half_t*)a.kmin + off);
+            hi[r] = *(const u4*)((const half_t*)a.kmax + off);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float bst = neg_inf();
+#pragma unroll
+            for (int q = 0; q < COOP_MAX_NREP; ++q) {
+                // (a uniform branch, the loop fully unrolled: the rows stay
+                // in registers; a `break` here kept them in scratch)
+                if (q < a.NR) bst = fmaxf(bst, quest_row16_sum(quest_part(qv[q], qm[q], lo[r], hi[r])));
+            }
+            if ((lane & 15) == 0 && st[r] != 0) {
+                const float v = st[r] == 1 ? bst : st[r] == 2 ? __builtin_inff() : neg_inf();
+                __hip_atomic_store(srow + pg[r], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
+// One page's score computed alone by the calling thread (the same sums in
+// the same order as score_slice), for a score that did not arrive in time.
+__device__ float score_one(const DecodeParams& a, int b, int h, int len, int p) {
+    const int np = len > 0 ? (len + PAGE - 1) / PAGE : 0;
+    if (p >= np) return neg_inf();
+    if (p == 0 || p >= np - a.recent) return __builtin_inff();
+    const int blk = p < a.max_pages ? a.block_tables[(int64_t)b * a.sbt_b + p] : -1;
+    if ((unsigned)blk >= (unsigned)a.num_blocks) return neg_inf();
+    const half_t* qb = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h;
+    const half_t* lob = (const half_t*)a.kmin + (int64_t)blk * a.sb_b + (int64_t)h * a.sb_h;
+    const half_t* hib = (const half_t*)a.kmax + (int64_t)blk * a.sb_b + (int64_t)h * a.sb_h;
+    // quest_row16_sum's order as lane 0 sees it: lane pairs (xor 1), pairs
+    // of pairs (xor 2), the half-row mirror, the row mirror, i.e. the pairs
+    // (0,1) (2,3) | (6,7) (4,5) || (14,15) (12,13) | (8,9) (10,11) combined
+    // left to right at each level; taken one pair at a time so only one
+    // pair's operands are live
+    float bst = neg_inf();
+    for (int q = 0; q < a.NR; ++q) {
+        const half_t* qr = qb + (int64_t)q * a.sq_r;
+        float pa = 0.f, qa = 0.f, ha = 0.f, tot = 0.f;
+#pragma unroll 1
+        for (int k = 0; k < 8; ++k) {
+            const int m = (k & 4 ? 8 : 0) + ((k & 2) ? (k & 1 ? 4 : 6) : (k & 1 ? 2 : 0)) ^
+                          (k & 4 ? 6 : 0);
+            const float x = quest_part(*(const u4*)(qr + 8 * m), *(const u4*)(lob + 8 * m),
+                                       *(const u4*)(hib + 8 * m));
+            const float y = quest_part(*(const u4*)(qr + 8 * (m + 1)),
+                                       *(const u4*)(lob + 8 * (m + 1)),
+                                       *(const u4*)(hib + 8 * (m + 1)));
+            const float v = x + y;
+            if ((k & 1) == 0) {
+                pa = v;
+            } else {
+                const float qd = pa + v;
+                if ((k & 2) == 0) {
+                    qa = qd;
+                } else {
+                    const float hv = qa + qd;
+                    if ((k & 4) == 0) ha = hv;
+                    else tot = ha + hv;
+                }
+            }
+        }
+        bst = fmaxf(bst, tot);
+    }
+    return bst;
+}
+
 // SPARSE: 0 the dense walk; 1 a page-subset walk over the caller's lists;
-// 2 a page-subset walk whose lists the group selects from page scores.
+// 2 a page-subset walk whose lists the group selects from page scores;
+// 3 the same with the scores computed by the launch itself, each group
+// scoring its share of its sequence's pages (score_slice).
 template <int KIND, bool ASYM, bool HAS_RES, int SPARSE, int NWT, int HG, int ABL = 0>
 __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodeParams a) {
     // Pages in flight ahead of the one being computed.  INT8 keeps one: a
@@ -751,7 +863,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     };
     auto fill_table = [&]() {
         if (!cached) return;
-        if constexpr (SPARSE == 2) {
+        if constexpr (SPARSE >= 2) {
             // Each 256-thread half selects its head's list from the page
             // scores (the selection kernel's radix select; in LDS the merge
             // buffer holds only after the walk) and keeps the entries of
@@ -763,7 +875,8 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             static_assert(WAVE * NWT == 256 * HG, "one 256-thread group a head");
             static_assert(CAP >= SELECT_SPLIT_ENTRIES, "a split's entries fit the table");
             const int hh = threadIdx.x / 256, tid = threadIdx.x % 256;
-            SelectSmem* ssm = reinterpret_cast<SelectSmem*>(&sm.acc[0][0][0][0]);
+            static_assert(sizeof(LinSelectSmem) * HG <= sizeof(sm.acc), "selection fits the merge buffer");
+            LinSelectSmem* ssm = reinterpret_cast<LinSelectSmem*>(&sm.acc[0][0][0][0]);
             const float* row = a.scores + (int64_t)b * a.ssc_b + (int64_t)(h0 + hh) * a.ssc_h;
             // the selection reports pages only; their blocks are looked up
             // below, one independent load a thread (a load per reported page
@@ -771,13 +884,54 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             auto emit = [&](int pos, int pg) {
                 if (pos >= lo && pos < hi) sm.ent[(hh * 2 + 1) * CAP + pos - lo] = pg;
             };
-            if (a.score_pages <= 8 * 256)
-                select_row_k<false, 8>(row, a.score_pages, n_list, 0, tid, nullptr, ssm[hh],
-                                       nullptr, emit);
-            else
-                select_row_k<false, 32>(row, a.score_pages, n_list, 0, tid, nullptr, ssm[hh],
-                                        nullptr, emit);
+            if constexpr (SPARSE == 3) {
+                // this group's share of the sequence's pages scored, then the
+                // whole rows read as the other groups' shares land
+                const int per = (a.score_pages + Sb - 1) / Sb;
+                const int p_lo = gw.s * per;
+                const int p_hi = p_lo + per < a.score_pages ? p_lo + per : a.score_pages;
+                score_slice<NWT, HG>(a, b, h0, len, p_lo, p_hi);
+                // the group's score stores complete, then it counts itself in
+                // the word after row (b, h0) (all ones at rest, so the count
+                // reaches Sb - 1 when every group of the sequence is done)
+                int* done = (int*)(a.scores + (int64_t)b * a.ssc_b + (int64_t)h0 * a.ssc_h +
+                                   a.score_pages);
+                handoff_release();
+                __syncthreads();
+                if (threadIdx.x == 0)
+                    __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                struct Coop {
+                    const DecodeParams& a;
+                    int b, h, len, Sb;
+                    const int* done;
+                    __device__ float operator()(int p) const { return score_one(a, b, h, len, p); }
+                    __device__ void wait() const {
+                        // one word polled (every thread of a wave reads the same line)
+                        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+                        while (load_coherent(done) != Sb - 1 &&
+                               __builtin_amdgcn_s_memrealtime() - t0 < COOP_WAIT_TICKS)
+                            __builtin_amdgcn_s_sleep(8);
+                    }
+                };
+                const Coop fix{a, b, h0 + hh, len, Sb, done};
+                // (rows of up to COOP_MAX_PAGES pages, eight keys a thread)
+                select_row_lin<8, decltype(emit), 1>(row, a.score_pages, n_list, tid, ssm[hh],
+                                                     emit, fix);
+            } else {
+                if (a.score_pages <= 8 * 256)
+                    select_row_lin<8>(row, a.score_pages, n_list, tid, ssm[hh], emit);
+                else
+                    select_row_lin<32>(row, a.score_pages, n_list, tid, ssm[hh], emit);
+            }
             __syncthreads();
+            if (SPARSE == 3 && Sb == 1) {
+                // the only reader of its rows: back to all ones (with the
+                // count after row (b, h0))
+                for (int p = tid; p <= a.score_pages; p += 256)
+                    __hip_atomic_store((uint32_t*)(a.scores + (int64_t)b * a.ssc_b +
+                                                   (int64_t)(h0 + hh) * a.ssc_h + p),
+                                       EMPTY_WORD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             const int32_t* trow = a.block_tables + (int64_t)b * a.sbt_b;
             for (int i = threadIdx.x; i < n_ent * HG; i += WAVE * NWT) {
                 const int hs = i / n_ent, e = i % n_ent;
@@ -905,7 +1059,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         // The first items are fixed (wave wv takes wv, wv + NWT, ...): their
         // loads are in flight while the group fills the item table and meets
         // at the barrier (a selecting group knows its items only after).
-        if (SPARSE == 2) {
+        if (SPARSE >= 2) {
             fill_table();
             __syncthreads();
         }
@@ -913,7 +1067,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         for (int u = 0; u < PF_DEPTH; ++u)
             issue_with([&](int i, int& blk, int& pg, int& hh) { first(u, i, blk, pg, hh); }, u,
                        wv + u * NWT);
-        if (SPARSE != 2) {
+        if (SPARSE < 2) {
             fill_table();
             __syncthreads();
         }
@@ -956,7 +1110,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     auto first_fixed = [&](int u, int i, int& blk, int& pg, int& hh) { resolve_first(u, i, blk, pg, hh); };
     auto first_mem = [&](int, int i, int& blk, int& pg, int& hh) { resolve_mem(i, blk, pg, hh); };
     auto first_lds = [&](int, int i, int& blk, int& pg, int& hh) { resolve_lds(i, blk, pg, hh); };
-    if (SPARSE == 2)
+    if (SPARSE >= 2)
         walk(resolve_lds, first_lds);      // the host keeps every range within the table
     else if (cached && spec_ok)
         walk(resolve_lds, first_fixed);
@@ -1095,6 +1249,14 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // every group of this (b, h) has arrived: back to zero for the next launch
     if (t256 == 0)
         __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (SPARSE == 3) {
+        // and every group has read this row's scores: back to all ones (with
+        // the count after row (b, h0))
+        for (int p = t256; p <= a.score_pages; p += 256)
+            __hip_atomic_store((uint32_t*)(a.scores + (int64_t)b * a.ssc_b +
+                                           (int64_t)(h0 + hh) * a.ssc_h + p),
+                               EMPTY_WORD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 template <int VEC>
@@ -1159,6 +1321,7 @@ static int ablation() {
 #endif
 
 static hipError_t launch_kernel(const DecodeParams& a, hipStream_t stream) {
+    if (a.scores && a.kmin) return launch_t<KV_FP16, false, false, 3>(a, stream);
     if (a.scores) return launch_t<KV_FP16, false, false, 2>(a, stream);
     if (a.sel) return launch_t<KV_FP16, false, false, 1>(a, stream);
 #ifdef LS_DIAGNOSTICS

@@ -84,24 +84,78 @@ __device__ __forceinline__ uint32_t group_scan(uint32_t v, uint32_t* wsum, int t
 //
 // Every group of a workgroup passes the same barriers (a workgroup may run
 // one group a head): three a radix pass, one a scan after them.
-template <bool SORTED, int KPT, class Emit>
+//
+// COOP: the row is being written by other workgroups of the same launch
+// (the selecting decode's own scoring): after `fix.wait()` (the writers'
+// count, bounded in time) it is read with device-coherent loads, a word
+// still all ones (EMPTY_WORD, never a score) is read again until it lands,
+// and after COOP_WAIT_TICKS of the 100 MHz clock the missing scores are
+// computed by `fix(page)` instead (the same bits: the writers compute them
+// the same way), so no workgroup depends on another being resident.
+struct NoFix {
+    __device__ float operator()(int) const { return 0.f; }
+    __device__ void wait() const {}
+};
+constexpr uint64_t COOP_WAIT_TICKS = 5000;   // 50 us
+
+// A thread's KPT keys of the row (pages tid * KPT ...), as order keys;
+// `cnt` of them are real (the rest are past P).  COOP: the row is being
+// written by other workgroups of the same launch (described above).
+template <int KPT, int COOP, class Fix>
+__device__ __attribute__((always_inline)) void select_keys(const float* srow, int P, int tid,
+                                                           int i0, int cnt, uint32_t* key,
+                                                           Fix fix) {
+    // unconditional loads (clamped index) so they all issue back to back
+    float f[KPT];
+    const int last = P > 0 ? P - 1 : 0;
+    if constexpr (COOP) {
+        fix.wait();             // until the row's writers say they are done
+#pragma unroll
+        for (int j = 0; j < KPT; ++j)
+            f[j] = P > 0 ? load_coherent(srow + (i0 + j < last ? i0 + j : last)) : 0.f;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (true) {
+            bool missing = false;
+#pragma unroll
+            for (int j = 0; j < KPT; ++j)
+                missing = missing || (j < cnt && __builtin_bit_cast(uint32_t, f[j]) == EMPTY_WORD);
+            if (!missing) break;
+            // a round reads all of the thread's keys again, unconditionally:
+            // loads under per-key branches would each wait for the last
+            float g[KPT];
+#pragma unroll
+            for (int j = 0; j < KPT; ++j)
+                g[j] = load_coherent(srow + (i0 + j < last ? i0 + j : last));
+#pragma unroll
+            for (int j = 0; j < KPT; ++j)
+                f[j] = __builtin_bit_cast(uint32_t, f[j]) == EMPTY_WORD ? g[j] : f[j];
+            if (__builtin_amdgcn_s_memrealtime() - t0 > COOP_WAIT_TICKS) {
+#pragma unroll
+                for (int j = 0; j < KPT; ++j)
+                    if (j < cnt && __builtin_bit_cast(uint32_t, f[j]) == EMPTY_WORD)
+                        f[j] = fix(i0 + j);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) f[j] = P > 0 ? srow[i0 + j < last ? i0 + j : last] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) key[j] = j < cnt ? order_key(f[j]) : 0u;
+}
+
+template <bool SORTED, int KPT, class Emit, int COOP = 0, class Fix = NoFix>
 __device__ __attribute__((always_inline)) void select_row_k(const float* srow, int P, int n1,
                                                             int n2, int tid, int32_t* out,
                                                             SelectSmem& sm, uint32_t* skeys,
-                                                            Emit emit) {
+                                                            Emit emit, Fix fix = Fix()) {
     const int i0 = tid * KPT;
     int cnt = P - i0;
     cnt = cnt < 0 ? 0 : (cnt > KPT ? KPT : cnt);
     uint32_t key[KPT];
-    {
-        // unconditional loads (clamped index) so they all issue back to back
-        float f[KPT];
-        const int last = P > 0 ? P - 1 : 0;
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) f[j] = P > 0 ? srow[i0 + j < last ? i0 + j : last] : 0.f;
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) key[j] = j < cnt ? order_key(f[j]) : 0u;
-    }
+    select_keys<KPT, COOP>(srow, P, tid, i0, cnt, key, fix);
 
     // ---- radix select of the n1-th and n2-th largest keys ----
     uint32_t pre0 = 0, pre1 = 0, msk = 0;
@@ -163,6 +217,7 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
             shift = h - 7;
         }
     }
+    const bool two = n2 > 0;            // a second threshold to find
     for (int par = 0;; par ^= 1) {
         // (a pass below bit 0 repeats the bits of the last: the keys that
         // still match the prefix agree on them, so such a pass changes
@@ -185,7 +240,7 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
                     }
                     ++n0;
                 }
-                if ((key[j] & msk) == pre1) {
+                if (two && (key[j] & msk) == pre1) {
                     if (d != d1) {
                         if (n1c) atomicAdd(&sm.hist[par][1][d1], n1c);
                         d1 = d;
@@ -305,6 +360,258 @@ __device__ __attribute__((always_inline)) void select_row_k(const float* srow, i
     }
 }
 
+// ---- one threshold, linear bins ----
+//
+// The selecting decode needs only the n best pages of a row (no second
+// threshold, page order).  Its rows' finite scores span a narrow range, so
+// bins laid linearly over [min, max] of the finite candidate keys (order
+// keys: linear in the key, monotone in the score) put a handful of keys in
+// each: one round of histogram and scan finds the threshold bin, and the
+// few keys in it are ranked against each other directly.  A round is four
+// barriers (extrema, histogram, scan, threshold) against three a radix pass
+// plus the prefix stage, and one round usually decides what took the radix
+// select a prefix stage and two passes.  Bins: 0 for -inf (pages past the
+// end), 2047 for +inf (forced pages), 1..2046 linear.  A threshold bin that
+// is too full to rank directly (keys crowded by an outlier stretching the
+// range) gets another round over its own range.
+constexpr int LIN_BINS = 2048;
+constexpr int LIN_LIST = 64;            // a threshold bin this small is ranked directly
+
+struct LinSelectSmem {
+    // [round parity][bin]; past the bins, 32 words that take the adds of
+    // non-candidate keys (so every lane adds, without a branch)
+    uint32_t hist[2][LIN_BINS + 32];
+    uint32_t red[2][2][4];              // [round parity][min, max][wave]
+    uint32_t wsum[2][4];                // group_scan's wave totals
+    int found[2][4];                    // [round parity] bin, taken, its count, outcome
+    int list_n;
+    uint32_t list_key[LIN_LIST];        // (0 past list_n: never ahead of a real key)
+    int list_page[LIN_LIST];
+};
+
+// Min or max over a wave: within each row of 16 lanes by DPP (quad swaps,
+// half-row and row mirrors), then the four rows by readlane.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_extreme(uint32_t v) {
+    auto op = [](uint32_t x, uint32_t y) { return MAX ? (x > y ? x : y) : (x < y ? x : y); };
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return op(op(r0, r1), op(r2, r3));
+}
+
+// The n best pages of a row (n <= P), reported in page order through
+// emit(position, page); among equal scores the lower page first (the set
+// select_row_k reports for n1 = n, n2 = 0).  Same contract for the group,
+// COOP and `fix` as select_row_k; every group of the workgroup passes the
+// same barriers (the rounds go on while any group needs another).
+template <int KPT, class Emit, int COOP = 0, class Fix = NoFix>
+__device__ __attribute__((always_inline)) void select_row_lin(const float* srow, int P, int n,
+                                                              int tid, LinSelectSmem& sm,
+                                                              Emit emit, Fix fix = Fix()) {
+    // (written without per-key branches: selects and bit masks, one branch
+    // for the thread that reports the threshold; branchy forms of the same
+    // steps measured several times slower, each phase a chain of short
+    // divergent blocks)
+    static_assert(KPT <= 32, "a thread's keys fit a 32-bit mask");
+    constexpr int BPT = LIN_BINS / SEL_THREADS;           // bins a thread scans
+    static_assert(BPT == 8, "two 16-byte reads a thread");
+    constexpr uint32_t KEY_PINF = 0xFF800000u, KEY_NINF = 0x007FFFFFu;
+    enum { OPEN = 0, ALL = 1, NONE = 2, PAGE = 3, LIST = 4 };
+    const int i0 = tid * KPT;
+    int cnt = P - i0;
+    cnt = cnt < 0 ? 0 : (cnt > KPT ? KPT : cnt);
+    const uint32_t real = cnt >= 32 ? 0xFFFFFFFFu : (1u << cnt) - 1u;
+    const int wv = tid >> 6;
+    if (tid == 0) sm.list_n = 0;
+    if (tid < LIN_LIST) sm.list_key[tid] = 0u;
+    *(u4*)&sm.hist[0][tid * BPT] = u4{0u, 0u, 0u, 0u};
+    *(u4*)&sm.hist[0][tid * BPT + 4] = u4{0u, 0u, 0u, 0u};
+    uint32_t key[KPT];
+    select_keys<KPT, COOP>(srow, P, tid, i0, cnt, key, fix);
+
+    // candidates: the keys in [clo, chi]; keys above chi are taken, keys
+    // below clo are not, and `rem` of the candidates are taken
+    uint32_t clo = 0u, chi = 0xFFFFFFFFu;
+    int rem = n;
+    int mode = n > 0 ? OPEN : NONE;
+    int nscan = 0;
+    for (int par = 0;; par ^= 1) {
+        uint32_t cm = 0u;                                  // candidate keys
+        uint32_t kmn = 0xFFFFFFFFu, kmx = 0u;              // extrema of the finite ones
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            const uint32_t k = key[j];
+            const bool c = k >= clo && k <= chi;
+            cm |= (c ? 1u : 0u) << j;
+            const bool f = c && k != KEY_PINF && k != KEY_NINF && ((real >> j) & 1u);
+            const uint32_t lo = f ? k : 0xFFFFFFFFu, hi = f ? k : 0u;
+            kmn = lo < kmn ? lo : kmn;
+            kmx = hi > kmx ? hi : kmx;
+        }
+        cm &= mode == OPEN ? real : 0u;
+        kmn = wave_extreme<false>(kmn);
+        kmx = wave_extreme<true>(kmx);
+        if ((tid & 63) == 0) {
+            sm.red[par][0][wv] = kmn;
+            sm.red[par][1][wv] = kmx;
+        }
+        __syncthreads();
+        // (the other parity's histogram was last read before this barrier)
+        *(u4*)&sm.hist[par ^ 1][tid * BPT] = u4{0u, 0u, 0u, 0u};
+        *(u4*)&sm.hist[par ^ 1][tid * BPT + 4] = u4{0u, 0u, 0u, 0u};
+        uint32_t fmin = sm.red[par][0][0], fmax = sm.red[par][1][0];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            fmin = sm.red[par][0][w] < fmin ? sm.red[par][0][w] : fmin;
+            fmax = sm.red[par][1][w] > fmax ? sm.red[par][1][w] : fmax;
+        }
+        if (fmin > fmax) fmin = fmax = 0u;                 // no finite candidate
+        const uint32_t q = (fmax - fmin) / (uint32_t)(LIN_BINS - 2);
+        const int sh = q ? 32 - __builtin_clz(q) : 0;      // (fmax - fmin) >> sh <= 2045
+        const int spare = LIN_BINS + (tid & 31);
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            const uint32_t k = key[j];
+            uint32_t b = 1u + ((k - fmin) >> sh);
+            b = b < (uint32_t)(LIN_BINS - 2) ? b : (uint32_t)(LIN_BINS - 2);
+            b = k == KEY_PINF ? (uint32_t)(LIN_BINS - 1) : b;
+            b = k == KEY_NINF ? 0u : b;
+            atomicAdd(&sm.hist[par][((cm >> j) & 1u) ? (int)b : spare], 1u);
+        }
+        __syncthreads();
+        // this thread's bins, highest first: 2047 - 8 tid - j
+        const u4 b_lo = *(const u4*)&sm.hist[par][LIN_BINS - 8 - tid * BPT];
+        const u4 b_hi = *(const u4*)&sm.hist[par][LIN_BINS - 4 - tid * BPT];
+        const uint32_t c[BPT] = {b_hi.w, b_hi.z, b_hi.y, b_hi.x, b_lo.w, b_lo.z, b_lo.y, b_lo.x};
+        uint32_t tot = 0;
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) tot += c[j];
+        const int scan_par = nscan++ & 1;
+        const uint32_t incl = group_scan(tot, sm.wsum[scan_par], tid);
+        const uint32_t total = sm.wsum[scan_par][0] + sm.wsum[scan_par][1] +
+                               sm.wsum[scan_par][2] + sm.wsum[scan_par][3];
+        const uint32_t r = (uint32_t)rem;
+        uint32_t acc = incl - tot;
+        int fj = -1;
+        uint32_t fbefore = 0;
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) {
+            const bool hit = acc < r && acc + c[j] >= r;
+            fj = hit ? j : fj;
+            fbefore = hit ? acc : fbefore;
+            acc += c[j];
+        }
+        bool open = false;
+        if (mode == OPEN && r < total && fj >= 0) {
+            const int T = LIN_BINS - 1 - tid * BPT - fj;
+            const uint32_t cT = c[fj];
+            const int take = rem - (int)fbefore;
+            const int out = take == (int)cT                             ? ALL
+                            : (T == 0 || T == LIN_BINS - 1 || sh == 0) ? PAGE
+                            : cT <= (uint32_t)LIN_LIST                  ? LIST
+                                                                        : OPEN;
+            sm.found[par][0] = T;
+            sm.found[par][1] = take;
+            sm.found[par][2] = (int)cT;
+            sm.found[par][3] = out;
+            open = out == OPEN;
+        }
+        const bool more = __syncthreads_or(open);
+        if (mode == OPEN) {
+            if (r >= total) {
+                mode = ALL;                                // every candidate is taken
+            } else {
+                const int T = sm.found[par][0];
+                rem = sm.found[par][1];
+                mode = sm.found[par][3];
+                // the threshold bin's keys become the candidates
+                if (T == LIN_BINS - 1) {
+                    clo = KEY_PINF;
+                } else if (T == 0) {
+                    chi = KEY_NINF;
+                } else {
+                    // (within the finite extremes: ±inf keys stay outside)
+                    clo = fmin + ((uint32_t)(T - 1) << sh);
+                    const uint32_t top = clo + ((1u << sh) - 1u);
+                    chi = top < fmax ? top : fmax;
+                }
+            }
+        }
+        if (!more) break;
+    }
+    uint32_t am = 0u, cm = 0u;          // keys above; candidates
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+        const uint32_t k = key[j];
+        am |= (k > chi ? 1u : 0u) << j;
+        cm |= (k >= clo && k <= chi ? 1u : 0u) << j;
+    }
+    am &= real;
+    cm &= real;
+    // the threshold bin's keys ranked against each other: (key, page) pairs
+    // listed, each candidate counting the pairs ahead of it
+    if (mode == LIST) {
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            if ((cm >> j) & 1u) {
+                const int at = atomicAdd(&sm.list_n, 1);
+                if (at < LIN_LIST) {            // (the bin holds at most LIN_LIST)
+                    sm.list_key[at] = key[j];
+                    sm.list_page[at] = i0 + j;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t tm = mode == ALL ? cm : 0u;           // candidates taken (ALL, LIST)
+    if (mode == LIST) {
+        const int ln = sm.list_n < LIN_LIST ? sm.list_n : LIN_LIST;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            if ((cm >> j) & 1u) {
+                const uint32_t k = key[j];
+                const int pg = i0 + j;
+                int rank = 0;
+                for (int i = 0; i < ln; i += 4) {
+                    const u4 lk = *(const u4*)&sm.list_key[i];
+                    const u4 lp = *(const u4*)&sm.list_page[i];
+                    // (entries past ln hold key 0: never ahead)
+                    rank += (lk.x > k || (lk.x == k && (int)lp.x < pg)) ? 1 : 0;
+                    rank += (lk.y > k || (lk.y == k && (int)lp.y < pg)) ? 1 : 0;
+                    rank += (lk.z > k || (lk.z == k && (int)lp.z < pg)) ? 1 : 0;
+                    rank += (lk.w > k || (lk.w == k && (int)lp.w < pg)) ? 1 : 0;
+                }
+                tm |= (rank < rem ? 1u : 0u) << j;
+            }
+        }
+    }
+    // positions in page order: keys above and candidates taken before this
+    // thread's (PAGE: the first rem candidates in page order)
+    const uint32_t xm = mode == PAGE ? cm : tm;
+    const uint32_t v = (uint32_t)__builtin_popcount(am) | ((uint32_t)__builtin_popcount(xm) << 16);
+    const uint32_t ex = group_scan(v, sm.wsum[nscan++ & 1], tid) - v;
+    const int x_ex = (int)(ex >> 16);
+    if (mode == PAGE) {
+        // candidate j is taken when fewer than rem come before it
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            const int before = x_ex + __builtin_popcount(cm & ((1u << j) - 1u));
+            tm |= (((cm >> j) & 1u) && before < rem ? 1u : 0u) << j;
+        }
+    }
+    const uint32_t take = am | tm;
+    int pos = (int)(ex & 0xFFFFu) + (mode == PAGE ? (x_ex < rem ? x_ex : rem) : x_ex);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j)
+        if ((take >> j) & 1u) emit(pos++, i0 + j);
+}
+
 template <bool SORTED, class Emit>
 __device__ __attribute__((always_inline)) void select_row(const float* srow, int P, int n1, int n2,
                                                           int tid, int32_t* out, SelectSmem& sm,
@@ -322,6 +629,25 @@ __device__ __attribute__((always_inline)) void select_row(const float* srow, int
         select_row_k<SORTED, 16>(srow, P, n1, n2, tid, out, sm, skeys, emit);
     else
         select_row_k<SORTED, 32>(srow, P, n1, n2, tid, out, sm, skeys, emit);
+}
+
+// select_row_lin with the keys a thread holds fitted to the row length.
+template <class Emit>
+__device__ __attribute__((always_inline)) void select_lin(const float* srow, int P, int n, int tid,
+                                                          LinSelectSmem& sm, Emit emit) {
+    const int kpt = (P + SEL_THREADS - 1) / SEL_THREADS;
+    if (kpt <= 1)
+        select_row_lin<1>(srow, P, n, tid, sm, emit);
+    else if (kpt <= 2)
+        select_row_lin<2>(srow, P, n, tid, sm, emit);
+    else if (kpt <= 4)
+        select_row_lin<4>(srow, P, n, tid, sm, emit);
+    else if (kpt <= 8)
+        select_row_lin<8>(srow, P, n, tid, sm, emit);
+    else if (kpt <= 16)
+        select_row_lin<16>(srow, P, n, tid, sm, emit);
+    else
+        select_row_lin<32>(srow, P, n, tid, sm, emit);
 }
 
 }  // namespace ls

@@ -30,41 +30,13 @@
 #include "ls_common.h"
 #include "ls_sparse.h"
 #include "ls_select.h"
+#include "ls_quest.h"
 
 namespace ls {
 
 namespace {
 
 enum : int { PG_SKIP = 0, PG_SCORE = 1, PG_FORCED = 2, PG_PAST = 3 };
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                         0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over each row of 16 lanes, result in every lane of the row: quad
-// swaps (xor 1, xor 2), then half-row and row mirrors.
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dpp<0xB1>(v);
-    v += dpp<0x4E>(v);
-    v += dpp<0x141>(v);
-    v += dpp<0x140>(v);
-    return v;
-}
-
-// (Components are named, not indexed: subscripting a vector-typed reference
-// inside an unrolled loop lost all but the first component in this build.)
-__device__ __forceinline__ void h8_to_f8(u4 x, float* f) {
-    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const h2 t = __builtin_bit_cast(h2, w[i]);
-        f[2 * i] = (float)t.x;
-        f[2 * i + 1] = (float)t.y;
-    }
-}
-
 
 // NR: query rows per KV head (a compile-time count keeps only those rows'
 // registers, which sets how many index groups a CU holds at once).
@@ -109,25 +81,19 @@ __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
         }
     }
     const half_t* qb = (const half_t*)a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + c0;
-    u4 qv[NR];
+    u4 qv[NR], qm[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) qv[r] = *(const u4*)(qb + (int64_t)r * a.sq_r);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) qm[r] = quest_masks(qv[r]);
 
     float best[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        float lf[8], hf[8];
-        h8_to_f8(lo[i], lf);
-        h8_to_f8(hi[i], hf);
         float bst = neg_inf();
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            float qf[8];
-            h8_to_f8(qv[r], qf);
-            float s = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s += fmaxf(qf[j] * lf[j], qf[j] * hf[j]);
-            s = row16_sum(s);
+            const float s = quest_row16_sum(quest_part(qv[r], qm[r], lo[i], hi[i]));
             if (MASS)
                 bst = (lane & 15) == r ? s : bst;    // lane r of the row keeps head r
             else
@@ -248,6 +214,15 @@ __global__ __launch_bounds__(256) void page_select_kernel(SelectParams a) {
     auto emit = [&](int pos, int pg) {
         if ((unsigned)pos < (unsigned)k) out[pos] = pg;
     };
+    if constexpr (!SORTED) {
+        // one threshold (the whole list is the budget): the linear-bin search
+        // the selecting decode runs
+        __shared__ LinSelectSmem lsm;
+        if (n1 == k) {
+            select_lin(srow, a.P, n1, (int)threadIdx.x, lsm, emit);
+            return;
+        }
+    }
     select_row<SORTED>(srow, a.P, n1, a.k, (int)threadIdx.x, out, sm, skeys, emit);
 }
 
@@ -291,12 +266,12 @@ __global__ __launch_bounds__(256) void bounds_rebuild_kernel(BoundsParams a) {
 #pragma unroll
     for (int t = 0; t < PAGE; ++t) rows[t] = stream_load((const u4*)(src + (int64_t)t * a.s1));
     float mn[8], mx[8];
-    h8_to_f8(rows[0], mn);
-    h8_to_f8(rows[0], mx);
+    quest_h8_to_f8(rows[0], mn);
+    quest_h8_to_f8(rows[0], mx);
 #pragma unroll
     for (int t = 1; t < PAGE; ++t) {
         float f[8];
-        h8_to_f8(rows[t], f);
+        quest_h8_to_f8(rows[t], f);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             mn[j] = fminf(mn[j], f[j]);

@@ -5,13 +5,16 @@ Mirrors the reference's kernels/cuda/paged_sparse.py: ``budget`` (:74-78),
 (:104-123), ``select`` (:164-168), ``budgets`` (:171-182), ``sparse_decode``
 (:185-219) and ``sparse_attention`` (:222-251), all on HIP kernels.
 
-Per layer per decode step ``sparse_attention`` is two launches: the page
-index (scores) and a page-subset decode whose workgroups select their own
-lists from the scores (ls_sparse_attention_fp16: the selection kernel's
-radix select in each group's prologue, the same lists and partition as
-select + sparse_decode).  ``fused=False`` runs the three launches (index,
-select, decode) instead.  Nothing syncs with the host, so the step is
-capturable in a HIP graph.
+Per layer per decode step ``sparse_attention`` with bounds scoring is one
+launch (ls_sparse_attention_bounds_fp16): the page-subset decode's
+workgroups score their shares of their sequence's pages, exchange the
+scores, and each selects its own list with the selection kernel's radix
+select (the same lists and partition as index + select + sparse_decode).
+Mass scoring, and bounds scoring of rows longer than COOP_MAX_PAGES or of
+more than COOP_MAX_NREP query rows a KV head, are two launches (the scores,
+then ls_sparse_attention_fp16);
+``fused=False`` runs the three (index, select, decode).  Nothing syncs with
+the host, so the step is capturable in a HIP graph.
 """
 
 from __future__ import annotations
@@ -245,6 +248,10 @@ def sparse_decode(q, k_pool, v_pool, block_tables, seq_lens, sel,
 
 
 SELECT_SPLIT_ENTRIES = 1024    # list entries a selecting group keeps (a split's share)
+# the one-launch bounds path: rows of at most this many pages, at most this
+# many query rows a KV head (else the index kernel, then the selecting decode)
+COOP_MAX_PAGES = 2048
+COOP_MAX_NREP = 8
 
 
 def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
@@ -255,8 +262,10 @@ def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
                      out: Optional[torch.Tensor] = None, fused: bool = True) -> torch.Tensor:
     """Index, select, attend. The list width k follows `max_seq_len` (the
     context) when given, else the table's width; each sequence then attends
-    its own budget for its current length.  Two launches (the decode
-    selects), or three with ``fused=False``."""
+    its own budget for its current length.  Fused, bounds scoring is one
+    launch (the decode's workgroups score, select and attend) and mass
+    scoring two (the scores, then a decode that selects); ``fused=False``
+    runs index, select and decode as three."""
     if scoring not in ("bounds", "mass"):
         raise ValueError(f"unknown scoring {scoring!r} (bounds or mass)")
     page = k_pool.shape[1]
@@ -280,10 +289,6 @@ def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
     if block_tables.shape[1] > SELECT_MAX_PAGES:
         raise ValueError(f"selection supports up to {SELECT_MAX_PAGES} pages, "
                          f"got {block_tables.shape[1]}")
-    if scoring == "mass":
-        scores = page_scores_mass(q, kmin, kmax, block_tables, seq_lens, recent, softmax_scale)
-    else:
-        scores = page_scores(q, kmin, kmax, block_tables, seq_lens, recent)
     b, h, n_rep, d = q.shape
     splits = num_splits or pdh.choose_splits(b, h, k, q.device)
     splits = max(1, min(splits, max(1, k), pdh.MAX_SPLITS))
@@ -292,6 +297,26 @@ def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
     buf, work, cnt = pdh._buffers("sparse", b, h, splits, n_rep, q.device)
     target = buf if out is None else pdh.check_out(out, q)
     P, S = _lib.ptr, _lib.strides
+    if (scoring == "bounds" and block_tables.shape[1] <= COOP_MAX_PAGES
+            and n_rep <= COOP_MAX_NREP):
+        # one launch: the decode's workgroups score the pages themselves,
+        # exchanging the scores through a buffer kept all ones at rest
+        _check_bounds(kmin, kmax, q.device)
+        # (each row is followed by one word: the count of its scored shares)
+        ws = scratch("sparse_coop_scores", (b, h, block_tables.shape[1] + 1), torch.int32,
+                     q.device, init=-1)
+        rc = _lib.lib().ls_sparse_attention_bounds_fp16(
+            P(q), S(q, 3), P(k_pool), P(v_pool), S(k_pool, 3), k_pool.shape[0],
+            P(block_tables), block_tables.stride(0), block_tables.shape[1], P(seq_lens),
+            P(kmin), P(kmax), S(kmin, 2), P(ws), S(ws, 2), k, float(ratio), int(recent),
+            P(target), S(target, 3), P(work), P(cnt), b, h, n_rep, d, page,
+            splits, 0, float(scale), _lib.stream_of(q.device))
+        _lib.check(rc, "ls_sparse_attention_bounds_fp16")
+        return buf[:, :, :n_rep] if out is None else out
+    if scoring == "mass":
+        scores = page_scores_mass(q, kmin, kmax, block_tables, seq_lens, recent, softmax_scale)
+    else:
+        scores = page_scores(q, kmin, kmax, block_tables, seq_lens, recent)
     rc = _lib.lib().ls_sparse_attention_fp16(
         P(q), S(q, 3), P(k_pool), P(v_pool), S(k_pool, 3), k_pool.shape[0],
         P(block_tables), block_tables.stride(0), block_tables.shape[1], P(seq_lens),

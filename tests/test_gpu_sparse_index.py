@@ -314,3 +314,84 @@ def test_update_bounds_skips_slots_outside_the_pool():
     ps().update_bounds(k_new, slots, kmin, kmax)
     torch.cuda.synchronize()
     assert kmin.abs().sum().item() == 0 and kmax.abs().sum().item() == 0
+
+
+# ------------------------------------------- the decode's own selection ----
+def _crafted_scores(kind, b, h, p, lens, seed):
+    """Score rows that drive the selecting decode's threshold search through
+    each of its outcomes: a threshold bin taken whole, ranked directly, ties
+    taken in page order, another round over a crowded bin."""
+    rng = np.random.default_rng(seed)
+    s = rng.standard_normal((b, h, p)).astype(np.float32)
+    if kind == "ties":
+        s = np.round(s * 2) / 2                         # few values, many ties
+    elif kind == "equal":
+        s[:] = 1.5                                      # one finite value
+    elif kind == "outlier":
+        s[:, :, p // 2] = 1e30                          # stretches the range: a crowded bin
+        s[:, :, p // 3] = -1e30
+    elif kind == "forced":
+        s[:, :, : p // 2] = np.inf                      # more +inf pages than the budget
+    elif kind == "ulps":
+        # adjacent floats: keys one apart, bins of width one
+        s = (np.float32(1.0) + rng.integers(0, 40, (b, h, p)).astype(np.float32) *
+             np.finfo(np.float32).eps).astype(np.float32)
+    elif kind == "zeros":
+        s = np.where(rng.random((b, h, p)) < 0.5, np.float32(0.0), np.float32(-0.0))
+        s[:, :, ::7] = -1.0
+    elif kind == "dead":
+        s[:, :, 3::4] = -np.inf                         # dead pages inside the length
+    s[:, :, 0] = np.inf
+    for i, n in enumerate(lens):
+        np_ = -(-n // 16)
+        s[i, :, np_:] = -np.inf                         # past the end
+        s[i, :, max(0, np_ - 2):np_] = np.inf           # recent pages
+    return np.ascontiguousarray(s.astype(np.float32))
+
+
+@pytest.mark.parametrize("kind", ["normal", "ties", "equal", "outlier", "forced", "ulps",
+                                  "zeros", "dead"])
+@pytest.mark.parametrize("width,ratio,splits", [(2048, 0.5, 32), (300, 0.3, 4), (3000, 0.5, 8)])
+def test_selecting_decode_selects_what_select_does(kind, width, ratio, splits):
+    """The decode that selects from given scores attends exactly the lists
+    select() gives the list decode: bit-equal outputs (same lists, same split
+    partition), for score rows that exercise every outcome of its search."""
+    import ctypes
+    from latentserve_amd import _lib
+    from latentserve_amd.kernels.hip import paged_decode_hip as pdh
+    lens = [width * 16, width * 16 // 3 + 5, 40, 0]
+    q, k, v, t, l = paged_case(lens, h_kv=2, n_rep=6, seed=width, width=width)
+    Q, K, V, T, L = dev(q, k, v, t, l)
+    s = _crafted_scores(kind, len(lens), 2, width, lens, seed=width + len(kind))
+    S_ = dev(s)[0]
+    kk = ps().budget(ratio, width)
+    sel = ps().select(S_, kk, seq_lens=L, ratio=ratio)
+    want = ps().sparse_decode(Q, K, V, T, L, sel, num_splits=splits, ratio=ratio).clone()
+    b, h, n_rep, d = Q.shape
+    buf, work, cnt = pdh._buffers("sparse", b, h, splits, n_rep, Q.device)
+    P, St = _lib.ptr, _lib.strides
+    rc = _lib.lib().ls_sparse_attention_fp16(
+        P(Q), St(Q, 3), P(K), P(V), St(K, 3), K.shape[0], P(T), T.stride(0), T.shape[1], P(L),
+        P(S_), St(S_, 2), width, kk, float(ratio), 2, P(buf), St(buf, 3), P(work), P(cnt),
+        b, h, n_rep, d, 16, splits, 0, float(1.0 / np.sqrt(d)), _lib.stream_of(Q.device))
+    _lib.check(rc, "ls_sparse_attention_fp16")
+    torch.cuda.synchronize()
+    got = buf[:, :, :n_rep]
+    # (the waves claim pages dynamically: the same lists, merged in another
+    # order; the lists themselves are checked exactly through select())
+    err = (got.float() - want.float()).abs().max().item()
+    assert err < 1e-3, (kind, err)
+
+
+@pytest.mark.parametrize("kind", ["normal", "ties", "equal", "outlier", "forced", "ulps",
+                                  "zeros", "dead"])
+@pytest.mark.parametrize("p,k", [(2048, 1024), (300, 91), (3000, 1500), (5, 2), (600, 600)])
+def test_one_threshold_select_equals_the_oracle(kind, p, k):
+    """select() without a ratio takes one threshold (the search the selecting
+    decode runs): the top k in page order, ties to the lower page, exactly the
+    oracle's set."""
+    lens = [p * 16, p * 16 // 3 + 5, 40, 0]
+    s = _crafted_scores(kind, len(lens), 2, p, lens, seed=p + k + len(kind))
+    got = ps().select(dev(s)[0], k).cpu().numpy()
+    want = np.sort(oracle.select(s, k), axis=-1)
+    assert np.array_equal(got, want), kind
