@@ -185,8 +185,31 @@ __device__ __forceinline__ void compute_page(const PageBuf& buf, WaveState& st, 
             }
         } else {
             // the K scale row through the same slot
+            if (!ASYM) {
+                // as fp16 (the row's first 256 bytes), so the query is scaled
+                // with two packed fp16 multiplies a step (fp16(q) x fp16(s)
+                // rounded to fp16, against fp16(q x s) before: c4 36.1 ->
+                // 35.3 us).  Written and read as 32-bit words; the scale pair
+                // converted as one vector (converted one component at a
+                // time, this compiler packed the first twice).
+                typedef float f2 __attribute__((ext_vector_type(2)));
+                const h2 ksh = __builtin_convertvector(__builtin_bit_cast(f2, buf.ks), h2);
+                uint32_t* krow = (uint32_t*)&kscale[0][0];
+                krow[lane] = __builtin_bit_cast(uint32_t, ksh);
+#pragma unroll
+                for (int r = 0; r < 8; ++r) {
+                    const u4 kw = buf.k[r / 4];
+                    const uint32_t w = r % 4 == 0 ? kw.x : r % 4 == 1 ? kw.y : r % 4 == 2 ? kw.z : kw.w;
+                    const u2 kh = i8x4_to_h4(w);
+                    const int ch = 64 * (r / 4) + 16 * g + 4 * (r % 4);
+                    const h4 ks4 = as_h4(krow[ch / 2], krow[ch / 2 + 1]);
+                    s = mfma16(as_h4(kh.x, kh.y), qh[r] * ks4, s);
+                }
+            }
+        }
+        if (ASYM && !buf.res) {
             *(u2*)&kscale[0][2 * lane] = buf.ks;
-            if (ASYM) *(u2*)&kscale[1][2 * lane] = buf.kz;
+            *(u2*)&kscale[1][2 * lane] = buf.kz;
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 const u4 kw = buf.k[r / 4];
@@ -672,8 +695,9 @@ __device__ float score_one(const DecodeParams& a, int b, int h, int len, int p) 
 template <int KIND, bool ASYM, bool HAS_RES, int SPARSE, int NWT, int HG, int ABL = 0>
 __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodeParams a) {
     // Pages in flight ahead of the one being computed.  INT8 keeps one: a
-    // second buffer would take its kernels past 256 registers, to one wave
-    // per SIMD.
+    // second buffer measured slower (c4 35.3 -> 39.1 us; with the page loads
+    // as inline asm and the walk's own waits, 37.5 us at one head a group,
+    // spills at two), and a third takes the kernel to one wave a SIMD.
     constexpr int PF_DEPTH = KIND == KV_FP16 ? 2 : 1;
     constexpr int NB = PF_DEPTH + 1;
     __shared__ DecodeSmem<NWT, HG, KIND == KV_INT8> sm;
@@ -754,23 +778,17 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // is computed, and the item after is being claimed.
     PageBuf buf[NB];
     int item[NB], pgs[NB], blks[NB], hds[NB];
-    // An fp16 request needs only a block id that is safe to read: the item is
-    // checked against the sequence when it is computed.  (INT8 needs the
-    // page to pick its K source, so it checks first.)
-    auto issue_raw = [&](int slot, int it, int blk, int pg, int hh, bool ok, int rrow,
-                         int npages) {
+    auto issue_raw = [&](int slot, int it, int blk, int pg, int hh) {
         item[slot] = it;
         blks[slot] = blk;
         pgs[slot] = pg;
         hds[slot] = hh;
-        if (KIND == KV_FP16) {
-            const int safe_blk = (unsigned)blk < (unsigned)a.num_blocks ? blk : 0;
-            load_page<KIND, ASYM, HAS_RES>(a, buf[slot], safe_blk, -1, 0, 0, h0 + hh, g, c);
-        } else {
-            // (the walk never holds the residual page: it is computed apart)
-            load_page<KIND, ASYM, false>(a, buf[slot], ok ? blk : 0, ok ? pg : -1, npages, rrow,
-                                           h0 + hh, g, c);
-        }
+        // A request needs only a block id that is safe to read: the item is
+        // checked against the sequence when it is computed (and the walk
+        // never holds an INT8 sequence's residual page: it is computed apart)
+        const int safe_blk = (unsigned)blk < (unsigned)a.num_blocks ? blk : 0;
+        load_page<KIND, ASYM, KIND == KV_FP16 && HAS_RES>(a, buf[slot], safe_blk, -1, 0, 0,
+                                                          h0 + hh, g, c);
     };
     // Which sequence and split this group serves: the host grid's for a
     // page-subset walk, else the length-proportional deal.
@@ -1049,11 +1067,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         auto issue_with = [&](auto res, int slot, int it) {
             int blk, pg, hh;
             res(it, blk, pg, hh);
-            const bool ok = KIND == KV_FP16 ? true
-                                             : (it < n_items && blk >= 0 && blk < a.num_blocks &&
-                                                pg >= 0 && pg < num_pages &&
-                                                !(HAS_RES && pg == num_pages - 1 && !res_ok));
-            issue_raw(slot, it, blk, pg, hh, ok, res_row, num_pages);
+            issue_raw(slot, it, blk, pg, hh);
         };
         auto issue = [&](int slot, int it) { issue_with(resolve, slot, it); };
         // The first items are fixed (wave wv takes wv, wv + NWT, ...): their
