@@ -112,6 +112,20 @@ class Int8PagedKVCache(_PagedBase):
         for layer in self._pooled:
             layer[index] = 0
 
+    def shareable_blocks(self, index: int) -> int:
+        """Full pages whose K is quantized in the pool in every layer (a full
+        last page still has its K only in this slot's residual:
+        cache/int8_paged_cache.py:385-396)."""
+        return min(super().shareable_blocks(index), self.pooled_pages(index))
+
+    def attach_prefix(self, index: int, blocks: Sequence[int], num_tokens: int) -> None:
+        """As the fp16 cache; the attached pages are quantized (a prefix cache
+        only records shareable pages), so the slot's residual starts empty:
+        its next token opens a new page (cache/int8_paged_cache.py:398-413)."""
+        super().attach_prefix(index, blocks, num_tokens)
+        for layer in self._pooled:
+            layer[index] = len(blocks)
+
     def reset(self) -> None:
         super().reset()
         for layer in self._pooled:

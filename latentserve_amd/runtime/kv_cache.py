@@ -24,7 +24,7 @@ few list operations and one small copy.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Iterable, List, Optional, Sequence
+from typing import Callable, Iterable, List, Optional, Sequence
 
 import numpy as np
 import torch
@@ -41,6 +41,12 @@ class BlockAllocator:
     A fresh pool hands out 0, 1, 2, ...; a freed block is the next one
     handed out (most recently freed first).  Blocks are reference counted
     so a shared prefix can be held by several sequences.
+
+    Three optional hooks let a prefix cache lend the pool the blocks only it
+    still holds (cache/block_allocator.py:60-67, 100-103, 131-142):
+    ``reclaimable()`` counts them (admission sees them as available),
+    ``reclaimer(n)`` gives up to n of them back when an allocation comes up
+    short, and ``on_ref_change(block, old, new)`` reports every count change.
     """
 
     def __init__(self, num_blocks: int, block_size: int):
@@ -52,6 +58,9 @@ class BlockAllocator:
         self._refs: List[int] = [0] * self.num_blocks
         self._stack: List[int] = []
         self.peak_used = 0
+        self.reclaimer: Optional[Callable[[int], object]] = None
+        self.reclaimable: Optional[Callable[[], int]] = None
+        self.on_ref_change: Optional[Callable[[int, int, int], None]] = None
         self.reset()
 
     def reset(self) -> None:
@@ -74,8 +83,16 @@ class BlockAllocator:
     def blocks_for_tokens(self, num_tokens: int) -> int:
         return -(-int(num_tokens) // self.block_size)
 
+    @property
+    def num_available(self) -> int:
+        """What an allocation can get: free blocks, and blocks a prefix
+        cache holds alone."""
+        return len(self._stack) + (self.reclaimable() if self.reclaimable else 0)
+
     def allocate(self, count: int) -> List[int]:
         count = int(count)
+        if count > len(self._stack) and self.reclaimer is not None:
+            self.reclaimer(count - len(self._stack))
         if count > len(self._stack):
             raise OutOfBlocks(f"cannot allocate {count} blocks: only {len(self._stack)} of "
                               f"{self.num_blocks} are free")
@@ -91,17 +108,25 @@ class BlockAllocator:
             if not 0 <= b < self.num_blocks or self._refs[b] == 0:
                 raise ValueError(f"block {b} is free; only allocated blocks can be shared")
             self._refs[b] += 1
+            if self.on_ref_change is not None:
+                self.on_ref_change(b, self._refs[b] - 1, self._refs[b])
 
     def free(self, blocks: Iterable[int]) -> None:
+        """Drop one reference to each block; a block whose count reaches
+        zero goes back on the stack."""
         for b in blocks:
             if not 0 <= b < self.num_blocks or self._refs[b] == 0:
                 raise ValueError(f"block {b} is already free")
             self._refs[b] -= 1
             if self._refs[b] == 0:
                 self._stack.append(b)
+            if self.on_ref_change is not None:
+                self.on_ref_change(b, self._refs[b] + 1, self._refs[b])
 
-    def refcount(self, block: int) -> int:
+    def ref_count(self, block: int) -> int:
         return self._refs[block]
+
+    refcount = ref_count
 
 
 class BlockTable:
@@ -283,10 +308,35 @@ class _PagedBase:
         self._active = list(slots)
 
     def can_admit(self, num_tokens: int) -> bool:
-        return self.allocator.blocks_for_tokens(num_tokens) <= self.allocator.num_free
+        """Whether a prompt of num_tokens fits now (blocks a prefix cache
+        holds alone count: an allocation reclaims them)."""
+        return self.allocator.blocks_for_tokens(num_tokens) <= self.allocator.num_available
 
     def free_sequence(self, index: int) -> None:
         self.tables[index].free()
+
+    # ---- prefix sharing ---------------------------------------------------
+    def attach_prefix(self, index: int, blocks: Sequence[int], num_tokens: int) -> None:
+        """Start the empty slot `index` on `blocks`, whole pages already
+        written by another sequence with the same first num_tokens tokens
+        (cache/paged_cache.py:199-217).  The slot takes a reference to each;
+        pages are append-only, so a shared page is never written again."""
+        t = self.tables[index]
+        if t.length or t.blocks:
+            raise ValueError(f"slot {index} already holds a sequence")
+        if num_tokens != len(blocks) * self.block_size:
+            raise ValueError(f"a shared prefix is whole pages: {len(blocks)} pages hold "
+                             f"{len(blocks) * self.block_size} tokens, not {num_tokens}")
+        self.allocator.incref(blocks)
+        t.blocks = list(blocks)
+        t.length = int(num_tokens)
+        t.version += 1
+        t.lineage += 1
+
+    def shareable_blocks(self, index: int) -> int:
+        """Leading pages of slot `index` whose K/V in the pool is final, so a
+        prefix cache may hand them to another sequence."""
+        return self.tables[index].length // self.block_size
 
     def reset(self) -> None:
         """Forget every sequence; storage (and every address a graph holds)
