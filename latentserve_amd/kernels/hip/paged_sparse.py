@@ -191,16 +191,20 @@ def index_select(q, kmin, kmax, block_tables, seq_lens, k: int, ratio: float,
 
 
 def budget(ratio: float, max_pages: int, recent: int = 2) -> int:
-    """Pages kept per (sequence, KV head): at least the sink and recent ones."""
+    """List width for a context of max_pages pages: ceil(ratio x pages),
+    never fewer than page 0 plus the `recent` forced pages, never more than
+    the pages there are (paged_sparse.py:74-78)."""
     if ratio >= 1.0:
         return max_pages
     return min(max_pages, max(recent + 1, math.ceil(ratio * max_pages)))
 
 
 def budgets(seq_lens: torch.Tensor, ratio: float, recent: int = 2, page: int = 16) -> torch.Tensor:
-    """Per-sequence budget for its current length — the rule the sparse kernel
-    applies inline: max(recent + 1, ceil(ratio x pages)) in float32, capped at
-    the pages it has. For tests and reference; the kernel does not use it."""
+    """int32 [B]: how many pages each sequence attends at its present
+    length (paged_sparse.py:171-182).  The same product the kernels form in
+    fp32 with ceilf, so host and device agree on every length; raised to
+    recent + 1, cut to the sequence's pages.  The kernels compute it
+    themselves: this is for callers and tests."""
     pages = (seq_lens.to(torch.int64) + page - 1) // page
     if ratio >= 1.0:
         return pages.to(torch.int32)
