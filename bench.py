@@ -236,8 +236,47 @@ def cpu_baseline(cfg, tables, seq, layer, n_seqs):
         t0 = time.perf_counter()
         oracle.paged_decode(*args, num_splits=1, **extra)
         times.append(time.perf_counter() - t0)
-    return _cpu_result(cfg, lens, b, n, sorted(times)[1], threads,
-                       "C oracle paged_decode (num_splits=1)")
+    res = _cpu_result(cfg, lens, b, n, sorted(times)[1], threads,
+                      "C oracle paged_decode (num_splits=1)")
+    if cfg["kind"] == "fp16":
+        res["vectorised"] = cpu_gather_sdpa(q[:n], k, v, t, lens, b, threads, cfg)
+    return res
+
+
+def cpu_gather_sdpa(q, k, v, tables, lens, b, threads, cfg):
+    """The second CPU line: the reference's CPU gather path (each sequence's
+    pages gathered into contiguous K/V, then one fp32 attention of the n_rep
+    query rows of each KV head over them; model/attention/gqa.py:351-388,
+    cache/paged_cache.py:486-506), in torch on the same sample."""
+    import torch
+
+    torch.set_num_threads(threads)
+    kt, vt = torch.from_numpy(k), torch.from_numpy(v)
+    qt = torch.from_numpy(q).float()
+    n, h, r, d = qt.shape
+    page = kt.shape[1]
+    scale = 1.0 / math.sqrt(d)
+
+    def run():
+        for i in range(n):
+            L = int(lens[i])
+            idx = torch.from_numpy(tables[i, :-(-L // page)].astype("int64"))
+            kk = kt[idx].reshape(-1, h, d)[:L].float().transpose(0, 1)     # [h, L, d]
+            vv = vt[idx].reshape(-1, h, d)[:L].float().transpose(0, 1)
+            torch.nn.functional.scaled_dot_product_attention(qt[i], kk, vv, scale=scale)
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
+    sample_bytes = algorithmic_bytes(cfg, lens)
+    return {"value": round(sample_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "ms_per_layer_step": round(dt * 1e3 * b / n, 3),
+            "sample": f"{n} of {b} sequences, torch CPU gather + fp32 SDPA of the n_rep rows "
+                      f"of each KV head, median of 3 (after one untimed run)"}
 
 
 def host_cores() -> int:
