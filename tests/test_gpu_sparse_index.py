@@ -395,3 +395,33 @@ def test_one_threshold_select_equals_the_oracle(kind, p, k):
     got = ps().select(dev(s)[0], k).cpu().numpy()
     want = np.sort(oracle.select(s, k), axis=-1)
     assert np.array_equal(got, want), kind
+
+
+@pytest.mark.parametrize("h_kv,n_rep,width,lens,splits", [
+    (1, 1, 17, [17 * 16, 5, 0], 3),                     # one head a group, empty sequence
+    (2, 4, 300, [300 * 16, 2000, 1, 16], None),
+    (3, 8, 300, [4000, 300 * 16], 5),                   # odd heads: one head a group
+    (2, 6, 2048, [2048 * 16, 700], 32),                 # the bench's row length
+    (2, 6, 64, [64 * 16, 100], 64),                     # more splits than a row has list entries
+])
+def test_one_launch_bounds_path_matches_three_launches_and_the_oracle(h_kv, n_rep, width, lens,
+                                                                      splits):
+    """Bounds scoring in one launch (workgroups score, exchange, select and
+    attend) against index + select + list decode and against the oracle over
+    index_select's lists, across head counts, query rows, row lengths, split
+    counts and ragged lengths; twice, so the score buffer's reset is
+    exercised."""
+    q, k, v, t, l, kmin, kmax = index_case(lens, width=width, n_rep=n_rep, h_kv=h_kv,
+                                           seed=width + n_rep)
+    Q, K, V, T, L, KN, KX = dev(q, k, v, t, l, kmin, kmax)
+    ratio = 0.5
+    kk = ps().budget(ratio, width)
+    sel = ps().index_select(Q, KN, KX, T, L, kk, ratio).cpu().numpy()
+    want = oracle.sparse_decode(q, k, v, t, l, sel, ratio=ratio, recent=2)
+    for rep in range(2):
+        one = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=ratio, num_splits=splits)
+        three = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=ratio, num_splits=splits,
+                                      fused=False)
+        torch.cuda.synchronize()
+        assert_close(one.float().cpu().numpy(), want, ATOL, RTOL, f"one launch, rep {rep}")
+        assert (one.float() - three.float()).abs().max().item() < 1e-3, rep
