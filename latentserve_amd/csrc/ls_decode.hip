@@ -934,12 +934,13 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 const Coop fix{a, b, h0 + hh, len, Sb, done};
                 // (rows of up to COOP_MAX_PAGES pages, eight keys a thread)
                 select_row_lin<8, decltype(emit), 1>(row, a.score_pages, n_list, tid, ssm[hh],
-                                                     emit, fix);
+                                                     ssm[0].vote, emit, fix);
             } else {
                 if (a.score_pages <= 8 * 256)
-                    select_row_lin<8>(row, a.score_pages, n_list, tid, ssm[hh], emit);
+                    select_row_lin<8>(row, a.score_pages, n_list, tid, ssm[hh], ssm[0].vote, emit);
                 else
-                    select_row_lin<32>(row, a.score_pages, n_list, tid, ssm[hh], emit);
+                    select_row_lin<32>(row, a.score_pages, n_list, tid, ssm[hh], ssm[0].vote,
+                                       emit);
             }
             __syncthreads();
             if (SPARSE == 3 && Sb == 1) {
