@@ -582,20 +582,30 @@ __device__ __attribute__((always_inline)) void select_row_lin(const float* srow,
     uint32_t tm = mode == ALL ? cm : 0u;           // candidates taken (ALL, LIST)
     if (mode == LIST) {
         const int ln = sm.list_n < LIN_LIST ? sm.list_n : LIN_LIST;
+        // the first eight entries read once, by every thread, into registers
+        // (a bin usually holds a few keys): a per-candidate loop of LDS reads
+        // serialised one round trip after another across a wave's keys
+        // (entries past ln hold key 0: never ahead)
+        const u4 lk0 = *(const u4*)&sm.list_key[0], lk1 = *(const u4*)&sm.list_key[4];
+        const u4 lp0 = *(const u4*)&sm.list_page[0], lp1 = *(const u4*)&sm.list_page[4];
+        const uint32_t lk[8] = {lk0.x, lk0.y, lk0.z, lk0.w, lk1.x, lk1.y, lk1.z, lk1.w};
+        const uint32_t lp[8] = {lp0.x, lp0.y, lp0.z, lp0.w, lp1.x, lp1.y, lp1.z, lp1.w};
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
             if ((cm >> j) & 1u) {
                 const uint32_t k = key[j];
                 const int pg = i0 + j;
                 int rank = 0;
-                for (int i = 0; i < ln; i += 4) {
-                    const u4 lk = *(const u4*)&sm.list_key[i];
-                    const u4 lp = *(const u4*)&sm.list_page[i];
-                    // (entries past ln hold key 0: never ahead)
-                    rank += (lk.x > k || (lk.x == k && (int)lp.x < pg)) ? 1 : 0;
-                    rank += (lk.y > k || (lk.y == k && (int)lp.y < pg)) ? 1 : 0;
-                    rank += (lk.z > k || (lk.z == k && (int)lp.z < pg)) ? 1 : 0;
-                    rank += (lk.w > k || (lk.w == k && (int)lp.w < pg)) ? 1 : 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    rank += (lk[i] > k || (lk[i] == k && (int)lp[i] < pg)) ? 1 : 0;
+                for (int i = 8; i < ln; i += 4) {
+                    const u4 qk = *(const u4*)&sm.list_key[i];
+                    const u4 qp = *(const u4*)&sm.list_page[i];
+                    rank += (qk.x > k || (qk.x == k && (int)qp.x < pg)) ? 1 : 0;
+                    rank += (qk.y > k || (qk.y == k && (int)qp.y < pg)) ? 1 : 0;
+                    rank += (qk.z > k || (qk.z == k && (int)qp.z < pg)) ? 1 : 0;
+                    rank += (qk.w > k || (qk.w == k && (int)qp.w < pg)) ? 1 : 0;
                 }
                 tm |= (rank < rem ? 1u : 0u) << j;
             }
