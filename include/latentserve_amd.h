@@ -215,6 +215,14 @@ int ls_sparse_attention_bounds_fp16(const void* q, const int64_t* q_strides,
                                     int head_dim, int page, int num_splits, int max_seq_len,
                                     float softmax_scale, void* stream);
 
+/* Test hook, no counterpart in the reference: how long (ticks of the 100 MHz
+ * s_memrealtime clock, 5000 = 50 us by default) a workgroup of
+ * ls_sparse_attention_bounds_fp16 waits for the other workgroups' page scores
+ * before computing the missing ones itself.  Any value gives the same
+ * results (the scores are recomputed bit for bit); 0 forces the fallback.
+ * Process-wide; read at each call. */
+int ls_set_coop_wait_ticks(uint64_t ticks);
+
 /* Bytes of `workspace` ls_page_scores_mass needs: the per-head logits,
  * fp32 [batch, kv_heads, n_rep, max_pages]. */
 size_t ls_page_mass_workspace_bytes(int batch, int kv_heads, int n_rep, int max_pages);

@@ -28,7 +28,7 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
@@ -42,6 +42,7 @@ _SIGNATURES = {
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
     "ls_page_mass_workspace_bytes": [_I32, _I32, _I32, _I32],
+    "ls_set_coop_wait_ticks": [ctypes.c_uint64],
     "ls_page_scores_mass": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _VP, _I64P, _I32, _I32,
         _I32, _I32, _I32, _I32, _F32, _VP],

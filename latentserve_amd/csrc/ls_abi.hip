@@ -12,6 +12,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <string>
 
 #include "../../include/latentserve_amd.h"
@@ -229,7 +230,16 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 16; }
+int ls_abi_version(void) { return 17; }
+
+// The bound on the one-launch bounds path's wait for the other workgroups'
+// scores (ls_set_coop_wait_ticks).
+static std::atomic<uint64_t> g_coop_wait_ticks{ls::COOP_WAIT_TICKS};
+
+int ls_set_coop_wait_ticks(uint64_t ticks) {
+    g_coop_wait_ticks.store(ticks, std::memory_order_relaxed);
+    return LS_OK;
+}
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
     if (batch <= 0 || kv_heads <= 0 || n_rep <= 0 || num_splits <= 1) return 0;
@@ -465,6 +475,7 @@ int ls_sparse_attention_bounds_fp16(const void* q, const int64_t* q_strides,
     a.kmax = kmax;
     a.sb_b = bound_strides[0];
     a.sb_h = bound_strides[1];
+    a.coop_wait_ticks = g_coop_wait_ticks.load(std::memory_order_relaxed);
     a.num_sel = k;
     a.ratio = ratio;
     a.recent = recent;

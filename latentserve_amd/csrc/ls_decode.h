@@ -56,6 +56,8 @@ struct DecodeParams {
     const void* kmin;
     const void* kmax;
     int64_t sb_b, sb_h;
+    uint64_t coop_wait_ticks;          // how long (100 MHz ticks) a reader waits for the
+                                       // other groups' scores before scoring them itself
     float* work;                       // [B * S, H] records of NR*128 + 32 floats:
                                        // acc[NR][128], m[16] (natural log), l[16]
     int pages_per_split;               // > 0: dense walk partition given by the host

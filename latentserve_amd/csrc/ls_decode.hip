@@ -923,11 +923,12 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                     int b, h, len, Sb;
                     const int* done;
                     __device__ float operator()(int p) const { return score_one(a, b, h, len, p); }
+                    __device__ uint64_t ticks() const { return a.coop_wait_ticks; }
                     __device__ void wait() const {
                         // one word polled (every thread of a wave reads the same line)
                         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
                         while (load_coherent(done) != Sb - 1 &&
-                               __builtin_amdgcn_s_memrealtime() - t0 < COOP_WAIT_TICKS)
+                               __builtin_amdgcn_s_memrealtime() - t0 < a.coop_wait_ticks)
                             __builtin_amdgcn_s_sleep(8);
                     }
                 };

@@ -89,14 +89,14 @@ __device__ __forceinline__ uint32_t group_scan(uint32_t v, uint32_t* wsum, int t
 // (the selecting decode's own scoring): after `fix.wait()` (the writers'
 // count, bounded in time) it is read with device-coherent loads, a word
 // still all ones (EMPTY_WORD, never a score) is read again until it lands,
-// and after COOP_WAIT_TICKS of the 100 MHz clock the missing scores are
+// and after `fix.ticks()` of the 100 MHz clock the missing scores are
 // computed by `fix(page)` instead (the same bits: the writers compute them
 // the same way), so no workgroup depends on another being resident.
 struct NoFix {
     __device__ float operator()(int) const { return 0.f; }
     __device__ void wait() const {}
+    __device__ uint64_t ticks() const { return 0; }
 };
-constexpr uint64_t COOP_WAIT_TICKS = 5000;   // 50 us
 
 // A thread's KPT keys of the row (pages tid * KPT ...), as order keys;
 // `cnt` of them are real (the rest are past P).  COOP: the row is being
@@ -129,7 +129,7 @@ __device__ __attribute__((always_inline)) void select_keys(const float* srow, in
 #pragma unroll
             for (int j = 0; j < KPT; ++j)
                 f[j] = __builtin_bit_cast(uint32_t, f[j]) == EMPTY_WORD ? g[j] : f[j];
-            if (__builtin_amdgcn_s_memrealtime() - t0 > COOP_WAIT_TICKS) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > fix.ticks()) {
 #pragma unroll
                 for (int j = 0; j < KPT; ++j)
                     if (j < cnt && __builtin_bit_cast(uint32_t, f[j]) == EMPTY_WORD)

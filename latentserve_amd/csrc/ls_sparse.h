@@ -10,6 +10,10 @@ namespace ls {
 // Largest page count the selection keeps in registers (32 keys per thread of
 // a 256-thread group).
 constexpr int SELECT_MAX_PAGES = 8192;
+// How long a selecting decode that scores its own pages waits for the other
+// workgroups' scores before scoring the missing ones itself, by default
+// (100 MHz ticks: 50 us).
+constexpr uint64_t COOP_WAIT_TICKS = 5000;
 // Pages scored per index workgroup (4 waves x 2 rounds x 4 pages).
 constexpr int INDEX_PAGES_PER_GROUP = 32;
 

@@ -39,7 +39,7 @@ def test_python_binding_covers_the_header():
 
 
 def test_abi_version(lib):
-    assert lib.ls_abi_version() == 16
+    assert lib.ls_abi_version() == 17
 
 
 def test_workspace_size(lib):

@@ -425,3 +425,32 @@ def test_one_launch_bounds_path_matches_three_launches_and_the_oracle(h_kv, n_re
         torch.cuda.synchronize()
         assert_close(one.float().cpu().numpy(), want, ATOL, RTOL, f"one launch, rep {rep}")
         assert (one.float() - three.float()).abs().max().item() < 1e-3, rep
+
+
+@pytest.mark.parametrize("width,lens,splits", [(2048, [2048 * 16, 5000], 32), (300, [4800, 7], 5)])
+def test_one_launch_path_with_the_fallback_forced(width, lens, splits):
+    """With the wait bound at 0 every workgroup of the one-launch path scores
+    whatever it finds missing itself (the fallback that keeps a launch from
+    depending on its workgroups being resident together): the same output,
+    and the score buffer left all ones for the next call."""
+    from latentserve_amd import _lib
+    q, k, v, t, l, kmin, kmax = index_case(lens, width=width, seed=width + 1)
+    Q, K, V, T, L, KN, KX = dev(q, k, v, t, l, kmin, kmax)
+    ratio = 0.5
+    base = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=ratio, num_splits=splits).clone()
+    try:
+        _lib.lib().ls_set_coop_wait_ticks(0)
+        for _ in range(2):
+            forced = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=ratio, num_splits=splits)
+            torch.cuda.synchronize()
+            assert (forced.float() - base.float()).abs().max().item() < 1e-3
+    finally:
+        _lib.lib().ls_set_coop_wait_ticks(5000)
+    kk = ps().budget(ratio, width)
+    sel = ps().index_select(Q, KN, KX, T, L, kk, ratio).cpu().numpy()
+    want = oracle.sparse_decode(q, k, v, t, l, sel, ratio=ratio, recent=2)
+    assert_close(forced.float().cpu().numpy(), want, ATOL, RTOL, "fallback forced")
+    from latentserve_amd.kernels.gqa import _SCRATCH
+    for key, buf in _SCRATCH.items():
+        if key[0] == "sparse_coop_scores":
+            assert bool((buf == -1).all()), "score buffer not left all ones"
