@@ -224,9 +224,9 @@ def cpu_baseline(cfg, tables, seq, layer, n_seqs):
         return _cpu_result(cfg, lens, b, n, sorted(times)[1], threads,
                            "C oracle page_scores + stable top-k + sparse_decode")
     if cfg["kind"] == "int8":
-        q, kq, vq, ks, vs, res, rr = [x.cpu().numpy() for x in layer]
+        q, kq, vq, ks, vs, res_k, rr = [x.cpu().numpy() for x in layer]
         args = (q[:n], kq, vq, t, lens)
-        extra = dict(k_scale=ks, v_scale=vs, k_residual=res, res_rows=rr[:n])
+        extra = dict(k_scale=ks, v_scale=vs, k_residual=res_k, res_rows=rr[:n])
     else:
         q, k, v = [x.cpu().numpy() for x in layer]
         args = (q[:n], k, v, t, lens)
@@ -240,14 +240,19 @@ def cpu_baseline(cfg, tables, seq, layer, n_seqs):
                       "C oracle paged_decode (num_splits=1)")
     if cfg["kind"] == "fp16":
         res["vectorised"] = cpu_gather_sdpa(q[:n], k, v, t, lens, b, threads, cfg)
+    else:
+        res["vectorised"] = cpu_gather_sdpa(q[:n], kq, vq, t, lens, b, threads, cfg,
+                                            int8=(ks, vs, res_k, rr[:n]))
     return res
 
 
-def cpu_gather_sdpa(q, k, v, tables, lens, b, threads, cfg):
+def cpu_gather_sdpa(q, k, v, tables, lens, b, threads, cfg, int8=None):
     """The second CPU line: the reference's CPU gather path (each sequence's
-    pages gathered into contiguous K/V, then one fp32 attention of the n_rep
-    query rows of each KV head over them; model/attention/gqa.py:351-388,
-    cache/paged_cache.py:486-506), in torch on the same sample."""
+    pages gathered into contiguous K/V, dequantized for an INT8 pool with the
+    last page of K from the fp16 residual, then one fp32 attention of the
+    n_rep query rows of each KV head over them; model/attention/gqa.py:
+    351-388, cache/paged_cache.py:486-506, kernels/gqa/paged_decode.py:
+    122-148), in torch on the same sample."""
     import torch
 
     torch.set_num_threads(threads)
@@ -256,13 +261,26 @@ def cpu_gather_sdpa(q, k, v, tables, lens, b, threads, cfg):
     n, h, r, d = qt.shape
     page = kt.shape[1]
     scale = 1.0 / math.sqrt(d)
+    if int8 is not None:
+        kst, vst, krt = (torch.from_numpy(x) for x in int8[:3])
+        rows = int8[3]
+
+    def gather(i, L):
+        np_ = -(-L // page)
+        idx = torch.from_numpy(tables[i, :np_].astype("int64"))
+        if int8 is None:
+            kk = kt[idx].float()
+            vv = vt[idx].float()
+        else:
+            kk = kt[idx].float() * kst[idx][:, None]                       # [P, 16, h, d]
+            vv = vt[idx].float() * vst[idx][..., None]
+            kk[np_ - 1] = krt[int(rows[i])].float()                        # the residual page
+        return (kk.reshape(-1, h, d)[:L].transpose(0, 1),                 # [h, L, d]
+                vv.reshape(-1, h, d)[:L].transpose(0, 1))
 
     def run():
         for i in range(n):
-            L = int(lens[i])
-            idx = torch.from_numpy(tables[i, :-(-L // page)].astype("int64"))
-            kk = kt[idx].reshape(-1, h, d)[:L].float().transpose(0, 1)     # [h, L, d]
-            vv = vt[idx].reshape(-1, h, d)[:L].float().transpose(0, 1)
+            kk, vv = gather(i, int(lens[i]))
             torch.nn.functional.scaled_dot_product_attention(qt[i], kk, vv, scale=scale)
 
     run()
@@ -275,7 +293,8 @@ def cpu_gather_sdpa(q, k, v, tables, lens, b, threads, cfg):
     sample_bytes = algorithmic_bytes(cfg, lens)
     return {"value": round(sample_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
             "ms_per_layer_step": round(dt * 1e3 * b / n, 3),
-            "sample": f"{n} of {b} sequences, torch CPU gather + fp32 SDPA of the n_rep rows "
+            "sample": f"{n} of {b} sequences, torch CPU gather"
+                      f"{' + dequant' if int8 is not None else ''} + fp32 SDPA of the n_rep rows "
                       f"of each KV head, median of 3 (after one untimed run)"}
 
 
