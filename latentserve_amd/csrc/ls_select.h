@@ -1,11 +1,15 @@
 // Top-k page selection over a row of page scores, for a group of 256
-// threads: shared by the selection kernel (one group a row) and the sparse
-// decode kernel's selecting prologue (one group a head of its workgroup).
+// threads: the selection kernel (one group a row) and the selecting decodes'
+// prologues (one group a head of the workgroup).
 //
-// A radix select (8-bit digits, LDS histograms, up to 4 passes: it stops
-// once the threshold digit's bin is taken whole) finds the n-th largest
-// key of the row; the selected pages are reported in page order,
-// ties at the threshold taken in page order (deterministic).  Reference:
+// Two searches.  select_row_k, a radix select (8-bit digits, LDS
+// histograms, up to 4 passes: it stops once the threshold digit's bin is
+// taken whole), finds two thresholds at once (a sequence's own budget and
+// the list width) and can report the set best first; the selection kernel
+// uses it for those.  select_row_lin finds one threshold over linear bins
+// (described below it); the selecting decodes and the one-threshold
+// selection use it.  Either reports the selected pages in page order, ties
+// at the threshold taken in page order (deterministic).  Reference:
 // kernels/cuda/paged_sparse.py:164-168 (select = torch.topk) and the budget
 // rule of kernels/cuda/paged_sparse_fp16.cu:242-247.
 #pragma once
@@ -146,16 +150,16 @@ __device__ __attribute__((always_inline)) void select_keys(const float* srow, in
     for (int j = 0; j < KPT; ++j) key[j] = j < cnt ? order_key(f[j]) : 0u;
 }
 
-template <bool SORTED, int KPT, class Emit, int COOP = 0, class Fix = NoFix>
+template <bool SORTED, int KPT, class Emit>
 __device__ __attribute__((always_inline)) void select_row_k(const float* srow, int P, int n1,
                                                             int n2, int tid, int32_t* out,
                                                             SelectSmem& sm, uint32_t* skeys,
-                                                            Emit emit, Fix fix = Fix()) {
+                                                            Emit emit) {
     const int i0 = tid * KPT;
     int cnt = P - i0;
     cnt = cnt < 0 ? 0 : (cnt > KPT ? KPT : cnt);
     uint32_t key[KPT];
-    select_keys<KPT, COOP>(srow, P, tid, i0, cnt, key, fix);
+    select_keys<KPT, 0>(srow, P, tid, i0, cnt, key, NoFix());
 
     // ---- radix select of the n1-th and n2-th largest keys ----
     uint32_t pre0 = 0, pre1 = 0, msk = 0;
