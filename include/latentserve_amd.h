@@ -27,11 +27,11 @@
  *               slot among its KV head's B * num_splits workgroups, which
  *               the kernel deals to sequences in proportion to their
  *               lengths); needed only when num_splits > 1
- *   counters    int32 [B * H_kv] (larger is fine), zero before the first
- *               call; every call leaves it zero again (per (sequence, head):
- *               the count of split workgroups that have stored their
- *               partials).  Calls that share scratch must be ordered on one
- *               stream.
+ *   counters    int32 [ls_decode_counter_ints(B, H_kv)] (larger is fine), zero
+ *               before the first call; every call leaves it zero again (per
+ *               (sequence, head), one 128-byte line apart: the count of
+ *               split workgroups that have stored their partials).  Calls
+ *               that share scratch must be ordered on one stream.
  *   max_seq_len the longest sequence in the call (the caller's bound, e.g.
  *               a graph bucket); it sets the pages per split.  A sequence
  *               longer than it is still handled (its split is re-derived on
@@ -69,6 +69,12 @@ int ls_abi_version(void);
  * partial buffers in Python (kernels/gqa/paged_decode.py:783-787). */
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits);
 
+/* Length (int32 elements) of the arrival-counter array a decode call takes:
+ * 32 per (sequence, KV head), so that no two pairs' counters share a cache
+ * line.  No counterpart in the reference, whose split combine is a second
+ * launch (paged_decode.py:689-706). */
+size_t ls_decode_counter_ints(int batch, int kv_heads);
+
 /* fp16 paged decode.  Replaces paged_decode_fp16 + the Triton combine, i.e.
  * paged_decode_cuda() for an fp16 pool (kernels/cuda/paged_decode_cuda.py:202-252,
  * kernels/cuda/paged_decode_fp16.cu:55-64) behind paged_decode_attention
@@ -88,11 +94,11 @@ int ls_paged_decode_fp16(const void* q, const int64_t* q_strides, const void* k_
 /* fp16 paged decode that allocates nothing and takes no workspace or
  * counters: the same kernel as ls_paged_decode_fp16, its split records and
  * arrival counters in a fixed device array of the library (16 MiB of records
- * plus 65536 counters, held per GPU until the process ends).  No counterpart
+ * plus 65536 counter ints, held per GPU until the process ends).  No counterpart
  * in the reference: for callers that cannot allocate device memory (code
  * under graph capture, tight serving loops, harnesses that forbid it).
  * Returns LS_ERR_INVALID when ls_decode_workspace_bytes(batch, kv_heads,
- * n_rep, num_splits) exceeds 16 MiB or batch * kv_heads exceeds 65536.  The
+ * n_rep, num_splits) exceeds 16 MiB or batch * kv_heads exceeds 2048.  The
  * first call on a device looks the array up and clears its counters on
  * `stream`.  All calls on one GPU share the array: calls that overlap on
  * one GPU (concurrent streams) race. */

@@ -28,13 +28,14 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
     "ls_abi_version": [],
     "ls_last_error": [],
     "ls_decode_workspace_bytes": [_I32, _I32, _I32, _I32],
+    "ls_decode_counter_ints": [_I32, _I32],
     "ls_paged_decode_fp16": [
         _VP, _I64P, _VP, _VP, _I64P, _I32, _VP, _I64, _I32, _VP, _VP, _I64P,
         _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _VP],
@@ -135,6 +136,7 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = argtypes
             fn.restype = {"ls_last_error": ctypes.c_char_p,
                           "ls_decode_workspace_bytes": ctypes.c_size_t,
+                          "ls_decode_counter_ints": ctypes.c_size_t,
                           "ls_decode_gemm_workspace_bytes": ctypes.c_size_t,
                           "ls_argmax_workspace_bytes": ctypes.c_size_t,
                           "ls_page_mass_workspace_bytes": ctypes.c_size_t,

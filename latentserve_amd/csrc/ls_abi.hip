@@ -230,7 +230,7 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 17; }
+int ls_abi_version(void) { return 18; }
 
 // The bound on the one-launch bounds path's wait for the other workgroups'
 // scores (ls_set_coop_wait_ticks).
@@ -239,6 +239,11 @@ static std::atomic<uint64_t> g_coop_wait_ticks{ls::COOP_WAIT_TICKS};
 int ls_set_coop_wait_ticks(uint64_t ticks) {
     g_coop_wait_ticks.store(ticks, std::memory_order_relaxed);
     return LS_OK;
+}
+
+size_t ls_decode_counter_ints(int batch, int kv_heads) {
+    if (batch <= 0 || kv_heads <= 0) return 0;
+    return (size_t)batch * (size_t)kv_heads * ls::COUNTER_STRIDE;
 }
 
 size_t ls_decode_workspace_bytes(int batch, int kv_heads, int n_rep, int num_splits) {
@@ -274,11 +279,12 @@ int ls_paged_decode_fp16_noalloc(const void* q, const int64_t* q_strides, const 
                                  int batch, int kv_heads, int n_rep, int head_dim, int page,
                                  int num_splits, int max_seq_len, float softmax_scale,
                                  void* stream) {
-    if (batch > 0 && kv_heads > 0 && (int64_t)batch * kv_heads > ls::NOALLOC_COUNTERS)
+    if (batch > 0 && kv_heads > 0 &&
+        (int64_t)batch * kv_heads > ls::NOALLOC_COUNTERS / ls::COUNTER_STRIDE)
         return fail(LS_ERR_INVALID,
                     "ls_paged_decode_fp16_noalloc: batch * kv_heads = %lld exceeds the fixed "
                     "scratch's %d arrival counters",
-                    (long long)batch * kv_heads, ls::NOALLOC_COUNTERS);
+                    (long long)batch * kv_heads, ls::NOALLOC_COUNTERS / ls::COUNTER_STRIDE);
     const size_t need = ls_decode_workspace_bytes(batch, kv_heads, n_rep, num_splits);
     if (need > ls::NOALLOC_WORK_BYTES)
         return fail(LS_ERR_INVALID,

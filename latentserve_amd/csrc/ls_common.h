@@ -147,6 +147,20 @@ __device__ __forceinline__ void coherent_pin(T& v) {
     asm volatile("" : "+v"(v));
 }
 
+// Workgroup ids renumbered XCD-major.  The dispatcher deals a launch's
+// workgroups to the 8 XCDs in turn (linear id L goes to XCD L % 8, the
+// XCD's (L / 8)-th), so numbering the XCD's groups contiguously,
+//   u = (groups on XCDs before L % 8) + L / 8,
+// gives the groups of one sequence (adjacent u) one XCD and its L2: the
+// sequence's block table, query and split records stay in one cache.  A
+// bijection of [0, N) for any N; correctness never depends on where a
+// group actually runs, only the speed does.
+__device__ __forceinline__ int xcd_major(int L, int N) {
+    constexpr int XCDS = 8;
+    const int q = N / XCDS, rem = N % XCDS, x = L % XCDS;
+    return x * q + (x < rem ? x : rem) + L / XCDS;
+}
+
 __device__ __forceinline__ void handoff_release() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);

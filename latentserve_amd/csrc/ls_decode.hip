@@ -710,9 +710,15 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     const int n_hg = H / HG;
     const int wv = threadIdx.x / WAVE;
     const int lane = threadIdx.x % WAVE;
-    const int h0 = (blockIdx.x % n_hg) * HG;
-    const int split = blockIdx.x / n_hg;
-    const int hb = blockIdx.y;          // the host grid's sequence (speculation)
+    // the host grid (split * n_hg + head group, sequence); a dense walk's
+    // numbered XCD-major so the groups of a sequence share an XCD (c2
+    // 50.3 -> 49.8 us; the page-subset walks measured slower so, c5 50.0 ->
+    // 51.2 us, and keep the dispatch order)
+    const int L = blockIdx.x + gridDim.x * blockIdx.y;
+    const int wg = SPARSE ? L : xcd_major(L, gridDim.x * gridDim.y);
+    const int h0 = (wg % gridDim.x % n_hg) * HG;
+    const int split = wg % gridDim.x / n_hg;
+    const int hb = wg / gridDim.x;      // the host grid's sequence (speculation)
     const int g = lane >> 4, c = lane & 15;
     const int S = a.num_splits;
     if (threadIdx.x == 0) sm.claim = NB * NWT;      // items below were assigned statically
@@ -1145,9 +1151,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         __syncthreads();
         if (!single && threadIdx.x < (unsigned)HG) {
             const int64_t bh = (int64_t)b * H + h0 + threadIdx.x;
-            if (__hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
+            if (__hip_atomic_fetch_add(a.counters + bh * COUNTER_STRIDE, 1, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT) == Sb - 1)
-                __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(a.counters + bh * COUNTER_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
     }
@@ -1245,7 +1251,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     __syncthreads();
     if (threadIdx.x < (unsigned)HG) {
         const int64_t bh = (int64_t)b * H + h0 + threadIdx.x;
-        const int prev = __hip_atomic_fetch_add(a.counters + bh, 1, __ATOMIC_RELAXED,
+        const int prev = __hip_atomic_fetch_add(a.counters + bh * COUNTER_STRIDE, 1, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
         sm.is_last[threadIdx.x] = prev == Sb - 1;
     }
@@ -1264,7 +1270,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     }
     // every group of this (b, h) has arrived: back to zero for the next launch
     if (t256 == 0)
-        __hip_atomic_store(a.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.counters + bh * COUNTER_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if constexpr (SPARSE == 3) {
         // and every group has read this row's scores: back to all ones (with
         // the count after row (b, h0))

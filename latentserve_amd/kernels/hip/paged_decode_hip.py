@@ -122,7 +122,8 @@ def _buffers(tag: str, b: int, h: int, splits: int, n_rep: int, device):
     """Persistent output, split workspace and arrival counters for one shape
     (graph-address stable)."""
     out = scratch(f"{tag}_out", (b, h, MAX_NREP, HEAD_DIM), torch.float16, device)
-    cnt = scratch(f"{tag}_cnt", (b * h,), torch.int32, device, init=0)
+    cnt = scratch(f"{tag}_cnt", (_lib.lib().ls_decode_counter_ints(b, h),), torch.int32, device,
+                  init=0)
     if splits == 1:
         return out, None, cnt
     nbytes = _lib.lib().ls_decode_workspace_bytes(b, h, n_rep, splits)

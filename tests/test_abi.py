@@ -39,11 +39,13 @@ def test_python_binding_covers_the_header():
 
 
 def test_abi_version(lib):
-    assert lib.ls_abi_version() == 17
+    assert lib.ls_abi_version() == 18
 
 
 def test_workspace_size(lib):
     assert lib.ls_decode_workspace_bytes(16, 2, 6, 1) == 0
+    assert lib.ls_decode_counter_ints(16, 2) == 16 * 2 * 32
+    assert lib.ls_decode_counter_ints(0, 2) == 0
     assert lib.ls_decode_workspace_bytes(16, 2, 6, 8) == 16 * 2 * 8 * (6 * 128 + 32) * 4
 
 
@@ -83,3 +85,16 @@ def test_bad_arguments_are_rejected_before_launch(lib, over, needle):
 
 def test_zero_batch_is_a_no_op(lib):
     assert _call_fp16(lib, B=0) == 0
+
+
+def test_noalloc_refuses_more_pairs_than_its_counters(lib):
+    """The fixed scratch holds 65536 counter ints, one 128-byte line (32
+    ints) per (sequence, KV head): 2048 pairs; more are refused before any
+    device call."""
+    assert lib.ls_decode_counter_ints(2048, 1) == 65536
+    rc = lib.ls_paged_decode_fp16_noalloc(1024, _strides(1536, 768, 128), 4096, 8192,
+                                          _strides(4096, 256, 128), 10, 16, 4, 4, 32, 64,
+                                          _strides(1536, 768, 128), 1025, 2, 6, 128, 16, 1, 0,
+                                          0.088, None)
+    assert rc == 1
+    assert "arrival counters" in lib.ls_last_error().decode()

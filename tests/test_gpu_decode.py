@@ -44,7 +44,7 @@ def run_fp16(case, num_splits=None, max_len=None):
 
 def test_library_is_the_hip_build():
     from latentserve_amd import _lib
-    assert _lib.lib().ls_abi_version() == _lib.ABI_VERSION == 17
+    assert _lib.lib().ls_abi_version() == _lib.ABI_VERSION == 18
 
 
 @pytest.mark.parametrize("splits", [None, 1, 3, 64])
