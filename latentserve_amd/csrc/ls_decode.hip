@@ -75,7 +75,11 @@ struct DecodeSmem {
     // INT8: each wave's K scale (and zero point) row of the page it computes,
     // then its 16 tokens' V scales (and zero points)
     float kscale[SCALES ? NWT : 1][2][SCALE_ROW];
-    float acc[HG][NWT][MAX_NREP][ROW];
+    // 16-byte aligned, so the state rows move as ds_write_b128 / ds_read_b128
+    // (at the struct's default 4-byte alignment they split into ds_*2_b32
+    // pairs: twice the LDS instructions, in a bank pattern the padding does
+    // not spread)
+    alignas(16) float acc[HG][NWT][MAX_NREP][ROW];
     int ent[ENT_INTS];
     int is_last[HG];
     int claim;
