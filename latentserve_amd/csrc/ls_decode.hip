@@ -70,8 +70,9 @@ struct DecodeSmem {
     // moment its walk ends, while the others still resolve items.
     static constexpr int ROW = HEAD_DIM + 4;
     static constexpr int ENT_INTS = 2048 * HG;
-    float m[HG][NWT][MAX_NREP];
-    float l[HG][NWT][MAX_NREP];
+    static constexpr int NWH = NWT / HG;     // waves a head
+    float m[HG][NWH][MAX_NREP];
+    float l[HG][NWH][MAX_NREP];
     // INT8: each wave's K scale (and zero point) row of the page it computes,
     // then its 16 tokens' V scales (and zero points)
     float kscale[SCALES ? NWT : 1][2][SCALE_ROW];
@@ -79,10 +80,10 @@ struct DecodeSmem {
     // (at the struct's default 4-byte alignment they split into ds_*2_b32
     // pairs: twice the LDS instructions, in a bank pattern the padding does
     // not spread)
-    alignas(16) float acc[HG][NWT][MAX_NREP][ROW];
+    alignas(16) float acc[HG][NWH][MAX_NREP][ROW];
     int ent[ENT_INTS];
     int is_last[HG];
-    int claim;
+    int claim[HG];
 };
 
 // Registers of one page for one wave.  K/V as raw dwords; INT8 rows are half
@@ -725,7 +726,13 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     const int hb = wg / gridDim.x;      // the host grid's sequence (speculation)
     const int g = lane >> 4, c = lane & 15;
     const int S = a.num_splits;
-    if (threadIdx.x == 0) sm.claim = NB * NWT;      // items below were assigned statically
+    // Each head of the group has its own NWH waves (wave wv serves head hw
+    // of the pair as its wl-th wave): a wave holds one head's state and
+    // query, and both heads' waves walk the same pages at about the same
+    // time, so the two halves of a token row are still read together.
+    constexpr int NWH = NWT / HG;
+    const int hw = wv / NWH, wl = wv % NWH;
+    if (threadIdx.x < (unsigned)HG) sm.claim[threadIdx.x] = NB * NWH;   // below: fixed items
 
     // Dense walk with pages-per-split given by the host (from the caller's
     // max_seq_len): the group's block ids are requested before the sequence
@@ -749,7 +756,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         // ... and lane u < NB of each wave fetches the block of the wave's
         // own fixed item u, so its first page loads need neither the table
         // nor the barrier.
-        const int e = (wv + (lane < NB ? lane : 0) * NWT) / HG;
+        const int e = wl + (lane < NB ? lane : 0) * NWH;
         const int fe = spec_lo + e;
         const int fv = row[fe < last ? fe : last];
         first_blk = lane < NB && e < a.pages_per_split && fe <= last ? fv : -1;
@@ -765,40 +772,36 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // free of any use before the first pages are requested.
     // (The host grid's sequence, which the deal keeps for equal lengths, so
     // the loads need not wait for the deal; reloaded below if it moved.)
-    h4 qh[HG][8];
+    h4 qh[8];
     // (INT8: the channel order of its K loads, 64(r/4) + 16g + 4(r%4) for
     // MFMA step r.)
     auto load_q = [&](int bq) {
-#pragma unroll
-    for (int hh = 0; hh < HG; ++hh) {
-        const half_t* qrow = a.q + (int64_t)bq * a.sq_b + (int64_t)(h0 + hh) * a.sq_h +
+        const half_t* qrow = a.q + (int64_t)bq * a.sq_b + (int64_t)(h0 + hw) * a.sq_h +
                              (int64_t)(c < a.NR ? c : 0) * a.sq_r;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const u4 t = KIND == KV_FP16 ? *(const u4*)(qrow + 8 * g + 32 * j)
                                          : *(const u4*)(qrow + 16 * g + 64 * (j / 2) + 8 * (j % 2));
-            qh[hh][2 * j] = as_h4(t.x, t.y);
-            qh[hh][2 * j + 1] = as_h4(t.z, t.w);
+            qh[2 * j] = as_h4(t.x, t.y);
+            qh[2 * j + 1] = as_h4(t.z, t.w);
         }
-    }
     };
     load_q(hb);
 
     // Page buffers in rotation: items k+1 and k+2 are in flight while item k
     // is computed, and the item after is being claimed.
     PageBuf buf[NB];
-    int item[NB], pgs[NB], blks[NB], hds[NB];
-    auto issue_raw = [&](int slot, int it, int blk, int pg, int hh) {
+    int item[NB], pgs[NB], blks[NB];
+    auto issue_raw = [&](int slot, int it, int blk, int pg) {
         item[slot] = it;
         blks[slot] = blk;
         pgs[slot] = pg;
-        hds[slot] = hh;
         // A request needs only a block id that is safe to read: the item is
         // checked against the sequence when it is computed (and the walk
         // never holds an INT8 sequence's residual page: it is computed apart)
         const int safe_blk = (unsigned)blk < (unsigned)a.num_blocks ? blk : 0;
         load_page<KIND, ASYM, KIND == KV_FP16 && HAS_RES>(a, buf[slot], safe_blk, -1, 0, 0,
-                                                          h0 + hh, g, c);
+                                                          h0 + hw, g, c);
     };
     // Which sequence and split this group serves: the host grid's for a
     // page-subset walk, else the length-proportional deal.
@@ -870,7 +873,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // the sequence computes it apart, so the walk's page buffers and compute
     // carry INT8 pages only (their residual branch cost 3 us at c4).
     const bool ends_seq = HAS_RES && n_ent > 0 && hi == num_pages;
-    const int n_items = (n_ent - (ends_seq ? 1 : 0)) * HG;
+    const int n_items = n_ent - (ends_seq ? 1 : 0);     // a head's items
 
     // Resolve the group's entries to (block, page) once, into LDS (the merge
     // buffer, idle until the walk ends).  Block ids outside the pool, list
@@ -1000,52 +1003,42 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
 
     const float scale_log2 = a.scale * LOG2E;
 
-    WaveState st[HG];
+    WaveState st;
 #pragma unroll
-    for (int hh = 0; hh < HG; ++hh) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) st[hh].acc[t] = (f4){0.f, 0.f, 0.f, 0.f};
-        st[hh].m = neg_inf();
-        st[hh].l = 0.f;
-        st[hh].z = 0.f;
-    }
+    for (int t = 0; t < 8; ++t) st.acc[t] = (f4){0.f, 0.f, 0.f, 0.f};
+    st.m = neg_inf();
+    st.l = 0.f;
+    st.z = 0.f;
 
-    // Item i: entry i / HG of head i % HG (the heads of a page are adjacent
-    // items, so a page's token rows are requested whole at about one time).
-    // Items past the end or unresolvable come back with blk -1: their buffer
-    // is filled from block 0 (any valid address: it keeps every iteration's
-    // loads and waits identical) and computed with every token masked.
-    auto resolve_lds = [&](int i, int& blk, int& pg, int& hh) {
-        hh = HG == 1 ? 0 : i % HG;
-        const int e = HG == 1 ? i : i / HG;
+    // Item i of the wave's head: entry i.  Items past the end or
+    // unresolvable come back with blk -1: their buffer is filled from block 0
+    // (any valid address: it keeps every iteration's loads and waits
+    // identical) and computed with every token masked.
+    auto resolve_lds = [&](int i, int& blk, int& pg) {
         if (i >= n_items) {
             blk = -1;
             pg = -1;
         } else if (SPARSE) {
-            blk = sm.ent[(hh * 2) * CAP + e];
-            pg = sm.ent[(hh * 2 + 1) * CAP + e];
+            blk = sm.ent[(hw * 2) * CAP + i];
+            pg = sm.ent[(hw * 2 + 1) * CAP + i];
         } else {
-            blk = sm.ent[e];
-            pg = lo + e;
+            blk = sm.ent[i];
+            pg = lo + i;
         }
     };
     // The wave's fixed item u (dense walk with the host's split): its block
     // is in lane u of first_blk.  Returned unchecked: the sequence length is
     // not needed to request the page (issue_with checks the item afterwards).
-    auto resolve_first = [&](int u, int i, int& blk, int& pg, int& hh) {
-        hh = HG == 1 ? 0 : i % HG;
-        const int e = HG == 1 ? i : i / HG;
-        pg = spec_lo + e;
+    auto resolve_first = [&](int u, int i, int& blk, int& pg) {
+        pg = spec_lo + i;
         blk = __builtin_amdgcn_readlane(first_blk, u);
     };
-    auto resolve_mem = [&](int i, int& blk, int& pg, int& hh) {
-        hh = HG == 1 ? 0 : i % HG;
-        const int e = HG == 1 ? i : i / HG;
+    auto resolve_mem = [&](int i, int& blk, int& pg) {
         if (i >= n_items) {
             blk = -1;
             pg = -1;
         } else {
-            resolve_global(e, hh, blk, pg);
+            resolve_global(i, hw, blk, pg);
         }
     };
 
@@ -1056,33 +1049,26 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     };
     auto walk = [&](auto resolve, auto first) {
         if constexpr (HAS_RES) {
-            // the last wave computes head h0's last page, the one before it
-            // head h0 + 1's
-            const int hr = NWT - 1 - wv;
-            if (ends_seq && res_ok && hr < HG) {
+            // the last wave of each head computes that head's last page
+            const int hr = hw;
+            if (ends_seq && res_ok && wl == NWH - 1) {
                 const int lp = num_pages - 1;
                 const int blk = a.block_tables[(int64_t)b * a.sbt_b + lp];
                 const bool okb = blk >= 0 && blk < a.num_blocks;
                 PageBuf rb;
                 load_page<KIND, ASYM, true>(a, rb, okb ? blk : 0, lp, num_pages, res_row, h0 + hr,
                                             g, c);
-                auto res_into = [&](int hh) {
-                    compute_page<KIND, ASYM>(rb, st[hh], qh[hh], okb ? lp : -1, okb ? len : 0,
-                                             scale_log2, g, sm.kscale[wv]);
-                };
-                if (HG == 1 || hr == 0)
-                    res_into(0);
-                else
-                    res_into(HG - 1);
+                compute_page<KIND, ASYM>(rb, st, qh, okb ? lp : -1, okb ? len : 0, scale_log2, g,
+                                         sm.kscale[wv]);
             }
         }
         auto issue_with = [&](auto res, int slot, int it) {
-            int blk, pg, hh;
-            res(it, blk, pg, hh);
-            issue_raw(slot, it, blk, pg, hh);
+            int blk, pg;
+            res(it, blk, pg);
+            issue_raw(slot, it, blk, pg);
         };
         auto issue = [&](int slot, int it) { issue_with(resolve, slot, it); };
-        // The first items are fixed (wave wv takes wv, wv + NWT, ...): their
+        // The first items are fixed (wave wl of a head takes wl, wl + NWH, ...): their
         // loads are in flight while the group fills the item table and meets
         // at the barrier (a selecting group knows its items only after).
         if (SPARSE >= 2) {
@@ -1091,20 +1077,19 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         }
 #pragma unroll
         for (int u = 0; u < PF_DEPTH; ++u)
-            issue_with([&](int i, int& blk, int& pg, int& hh) { first(u, i, blk, pg, hh); }, u,
-                       wv + u * NWT);
+            issue_with([&](int i, int& blk, int& pg) { first(u, i, blk, pg); }, u, wl + u * NWH);
         if (SPARSE < 2) {
             fill_table();
             __syncthreads();
         }
-        int it_n = wv + PF_DEPTH * NWT;
+        int it_n = wl + PF_DEPTH * NWH;
         if (item[0] >= n_items) return;
         while (true) {
 #pragma unroll
             for (int u = 0; u < NB; ++u) {
                 // claim an item (read next iteration), then load the item
                 // claimed last iteration into the free buffer
-                const int raw_new = claim_item(&sm.claim, lane);
+                const int raw_new = claim_item(&sm.claim[hw], lane);
                 issue((u + PF_DEPTH) % NB, it_n);
                 it_n = claimed_item(raw_new);
                 // computed even when dead (every token masked, a no-op on the
@@ -1112,19 +1097,11 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 // force conservative waits on the next reuse of its registers
                 const bool ok_u = live(u);
                 const int live_len = ok_u ? len : 0;
-                // the page goes to its head's state
-                auto take = [&](int hh) {
-                    if (ABL == 1 || ABL == 2)
-                        consume_page<KIND>(buf[u], st[hh]);
-                    else
-                        compute_page<KIND, ASYM>(buf[u], st[hh], qh[hh], ok_u ? pgs[u] : -1,
-                                                 live_len, scale_log2, g, sm.kscale[wv]);
-                };
-                static_assert(HG == 1 || HG == 2, "one or two heads a group");
-                if (HG == 1 || hds[u] == 0)
-                    take(0);
+                if (ABL == 1 || ABL == 2)
+                    consume_page<KIND>(buf[u], st);
                 else
-                    take(HG - 1);
+                    compute_page<KIND, ASYM>(buf[u], st, qh, ok_u ? pgs[u] : -1, live_len,
+                                             scale_log2, g, sm.kscale[wv]);
                 // items arrive in increasing order: past the end, all later are too
                 if (item[(u + 1) % NB] >= n_items) return;
             }
@@ -1133,9 +1110,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // Separate instantiations for the fast path (the host's split covers the
     // sequence and the item table fits in LDS) and the general ones, so no
     // fallback load shares the fast path's control flow.
-    auto first_fixed = [&](int u, int i, int& blk, int& pg, int& hh) { resolve_first(u, i, blk, pg, hh); };
-    auto first_mem = [&](int, int i, int& blk, int& pg, int& hh) { resolve_mem(i, blk, pg, hh); };
-    auto first_lds = [&](int, int i, int& blk, int& pg, int& hh) { resolve_lds(i, blk, pg, hh); };
+    auto first_fixed = [&](int u, int i, int& blk, int& pg) { resolve_first(u, i, blk, pg); };
+    auto first_mem = [&](int, int i, int& blk, int& pg) { resolve_mem(i, blk, pg); };
+    auto first_lds = [&](int, int i, int& blk, int& pg) { resolve_lds(i, blk, pg); };
     if (SPARSE >= 2)
         walk(resolve_lds, first_lds);      // the host keeps every range within the table
     else if (cached && spec_ok)
@@ -1149,9 +1126,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     const bool single = Sb == 1;
     const int w_rec = gw.first + gw.s;   // this group's record slot among the head group's B * S
     if (ABL >= 2) {                      // diagnostic: no merge, no partials
-#pragma unroll
-        for (int hh = 0; hh < HG; ++hh)
-            if (st[hh].acc[0][0] == 12345.f && st[hh].l == 1.f) a.out[threadIdx.x] = (half_t)st[hh].m;
+        if (st.acc[0][0] == 12345.f && st.l == 1.f) a.out[threadIdx.x] = (half_t)st.m;
         __syncthreads();
         if (!single && threadIdx.x < (unsigned)HG) {
             const int64_t bh = (int64_t)b * H + h0 + threadIdx.x;
@@ -1168,32 +1143,25 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // (w_rec * H + h); the groups of a sequence have adjacent slots.  Every
     // cache line of a record is written by this group alone.
     const int64_t rec = (int64_t)NR * HEAD_DIM + 2 * MAX_NREP;
-    float lrow[HG];
+    const float lrow = group4_sum(st.l);
+    if (ASYM) {
+        const float zrow = group4_sum(st.z);
 #pragma unroll
-    for (int hh = 0; hh < HG; ++hh) {
-        lrow[hh] = group4_sum(st[hh].l);
-        if (ASYM) {
-            const float zrow = group4_sum(st[hh].z);
-#pragma unroll
-            for (int t = 0; t < 8; ++t) st[hh].acc[t] += zrow;
-        }
+        for (int t = 0; t < 8; ++t) st.acc[t] += zrow;
     }
     if (c < NR) {                        // rows past n_rep hold nothing
+        if (g == 0) {
+            sm.m[hw][wl][c] = st.m;
+            sm.l[hw][wl][c] = lrow;
+        }
+        // the lane's 32 channels 32g..32g+31 (channel 32g + 8i + t is
+        // element i of tile t) as eight 16-byte stores
 #pragma unroll
-        for (int hh = 0; hh < HG; ++hh) {
-            if (g == 0) {
-                sm.m[hh][wv][c] = st[hh].m;
-                sm.l[hh][wv][c] = lrow[hh];
-            }
-            // the lane's 32 channels 32g..32g+31 (channel 32g + 8i + t is
-            // element i of tile t) as eight 16-byte stores
+        for (int j = 0; j < 8; ++j) {
+            f4 v;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                f4 v;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = st[hh].acc[4 * (j % 2) + e][j / 2];
-                *(f4*)&sm.acc[hh][wv][c][32 * g + 4 * j] = v;
-            }
+            for (int e = 0; e < 4; ++e) v[e] = st.acc[4 * (j % 2) + e][j / 2];
+            *(f4*)&sm.acc[hw][wl][c][32 * g + 4 * j] = v;
         }
     }
     __syncthreads();
@@ -1208,21 +1176,21 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         float* pm = pacc + NR * HEAD_DIM;
         float* pl = pm + MAX_NREP;
         for (int r = t256 / 32; r < NR; r += 8) {
-            float mv[NWT], lv[NWT];
-            f4 av[NWT];
+            float mv[NWH], lv[NWH];
+            f4 av[NWH];
 #pragma unroll
-            for (int u = 0; u < NWT; ++u) {
+            for (int u = 0; u < NWH; ++u) {
                 mv[u] = sm.m[hh][u][r];
                 lv[u] = sm.l[hh][u][r];
                 av[u] = *(const f4*)&sm.acc[hh][u][r][d0];
             }
             float mg = neg_inf();
 #pragma unroll
-            for (int u = 0; u < NWT; ++u) mg = fmaxf(mg, mv[u]);
+            for (int u = 0; u < NWH; ++u) mg = fmaxf(mg, mv[u]);
             float lt = 0.f;
             f4 at = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int u = 0; u < NWT; ++u) {
+            for (int u = 0; u < NWH; ++u) {
                 const float wt = mg == neg_inf() ? 0.f : fast_exp2(mv[u] - mg);
                 lt += lv[u] * wt;
 #pragma unroll
