@@ -1168,14 +1168,15 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
 
     // 256 threads a head; a thread merges four channels of one row, with
     // all of its loads issued together (rows 8 apart share a thread).
-    static_assert(WAVE * NWT == 256 * HG, "the merge is written for 256 threads a head");
+    // TPH threads a head (a multiple of 32: rows TPH / 32 apart share a thread)
+    constexpr int TPH = WAVE * NWH;
     {
-        const int hh = threadIdx.x / 256, t256 = threadIdx.x % 256;
+        const int hh = threadIdx.x / TPH, t256 = threadIdx.x % TPH;
         const int d0 = (t256 % 32) * 4;
         float* pacc = a.work + ((int64_t)w_rec * H + h0 + hh) * rec;
         float* pm = pacc + NR * HEAD_DIM;
         float* pl = pm + MAX_NREP;
-        for (int r = t256 / 32; r < NR; r += 8) {
+        for (int r = t256 / 32; r < NR; r += TPH / 32) {
             float mv[NWH], lv[NWH];
             f4 av[NWH];
 #pragma unroll
@@ -1228,9 +1229,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         sm.is_last[threadIdx.x] = prev == Sb - 1;
     }
     __syncthreads();
-    // 256 threads per head: a group of HG heads merges each head it closed
-    const int hh = threadIdx.x / 256, t256 = threadIdx.x % 256;
-    if (!sm.is_last[hh]) return;
+    // a group of HG heads merges each head it closed, 256 threads a head
+    const int hh = threadIdx.x / TPH, t256 = threadIdx.x % TPH;
+    if (!sm.is_last[hh] || t256 >= 256) return;
     const int64_t bh = (int64_t)b * H + h0 + hh;
     {
         // device-coherent loads: the records of groups on other XCDs
@@ -1273,16 +1274,13 @@ constexpr int NWAVES = 4;
 template <int KIND, bool ASYM, bool HAS_RES, int SPARSE, int ABL = 0>
 static hipError_t launch_t(const DecodeParams& a, hipStream_t stream) {
     // Heads in pairs when the head count allows: both halves of every token
-    // row are then read together.
-    // INT8 too (c4 37.0 -> 35.8 us), except asymmetric pools, whose zero
-    // points would push the two-head state past the register file (spills)
-    if constexpr (KIND == KV_FP16 || !ASYM) {
-        if (a.H % 2 == 0) {
+    // row are then read together (INT8 too: c4 37.0 -> 35.8 us).  Each wave
+    // holds one head's state, so asymmetric INT8's zero points fit as well.
+    if (a.H % 2 == 0) {
         dim3 grid(a.num_splits * (a.H / 2), a.B);
         hipLaunchKernelGGL((paged_decode_kernel<KIND, ASYM, HAS_RES, SPARSE, 2 * NWAVES, 2, ABL>),
                            grid, dim3(WAVE * NWAVES * 2), 0, stream, a);
         return hipGetLastError();
-        }
     }
     {
         dim3 grid(a.num_splits * a.H, a.B);

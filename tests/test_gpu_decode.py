@@ -219,9 +219,10 @@ def test_int8_matches_the_oracle(asym, res, splits):
 @pytest.mark.parametrize("h_kv", [1, 3, 4])
 @pytest.mark.parametrize("asym", [False, True])
 def test_int8_head_counts(h_kv, asym):
-    """Symmetric pools with an even head count take two heads a workgroup
-    (each head's last page from the residual by its own wave), odd counts
-    and asymmetric pools one: every head's output against the oracle."""
+    """An even head count takes two heads a workgroup (each head's last page
+    from the residual by a wave of its own half), an odd count one, for
+    symmetric and asymmetric pools: every head's output against the
+    oracle."""
     (q, k, v, t, l), ex = int8_case([700, 33, 16, 290], asym=asym, res=True, h_kv=h_kv,
                                     seed=11 + h_kv)
     want = oracle.paged_decode(q, k, v, t, l, num_splits=1, **ex)
