@@ -73,6 +73,11 @@ def parse():
                    help="instead of the benchmark, time the decode kernel's page compute alone "
                         "(MFMA, as built) against a VALU formulation, ITEMS pages a wave, from "
                         "the measurement build given by --diag-lib, and exit")
+    p.add_argument("--timeline", default=None, metavar="PATH",
+                   help="instead of the benchmark, run the config's layer launches from the "
+                        "-DLS_STAMPS build at PATH (python -m latentserve_amd.csrc.build "
+                        "--stamps PATH) and print where each launch's time goes, from every "
+                        "workgroup's clock stamps, then exit")
     p.add_argument("--diag-lib", default=None, metavar="PATH",
                    help="the -DLS_DIAGNOSTICS build (python -m latentserve_amd.csrc.build "
                         "--diagnostics PATH) that holds the page-compute probe")
@@ -378,6 +383,62 @@ def compute_probe(items, diag_lib):
     print(json.dumps(res))
 
 
+# The decode's stamp points (csrc/ls_decode.hip, ls_select.h; LS_STAMP).
+STAMP_NAMES = {0: "group start", 1: "own share scored", 2: "scores released, counted",
+               3: "peers' count seen", 4: "row keys loaded", 13: "extrema barrier",
+               14: "histogram barrier", 5: "threshold search done", 6: "list emitted",
+               7: "walk start", 8: "wave 0 walk end", 9: "waves merged, records stored",
+               10: "records released", 11: "arrival counted", 12: "combine done"}
+
+
+def timeline(cfg, args):
+    """Where one launch's time goes: every workgroup's stamps (100 MHz clock)
+    relative to the launch's first group start, median and spread over the
+    groups of several launches (the last of 8 layer launches each time, so
+    its pools are cold in L2 and MALL)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+    os.environ["LATENTSERVE_HIP_LIB"] = os.path.abspath(args.timeline)
+    tables, seq, pools, max_len = build_workload(cfg, 8)
+    calls = [make_call(cfg, tables, seq, lay, max_len, args.splits) for lay in pools]
+    for _ in range(20):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    lib = ctypes.CDLL(os.environ["LATENTSERVE_HIP_LIB"])
+    buf = np.zeros(8192 * 16, np.uint64)
+    rel, xcd_ok, groups = [], 0, 0
+    for _ in range(8):
+        for c in calls:
+            c()
+        torch.cuda.synchronize()
+        assert lib.ls_diag_read_stamps(buf.ctypes.data_as(ctypes.c_void_p),
+                                       ctypes.c_size_t(buf.nbytes)) == 0
+        st = buf.reshape(8192, 16).astype(np.int64)
+        t0 = st[:, 0]
+        last = np.where(t0 > t0.max() - 10000)[0]          # the last launch's groups
+        base = st[last, 0].min()
+        s = st[last, :15]
+        rel.append(np.where(s >= base, (s - base) * 0.01, np.nan))
+        xcd_ok += int(((last % 8) == (st[last, 15] & 15)).sum())
+        groups += len(last)
+    rel = np.concatenate(rel)
+    out = {"config": cfg["workload"], "launches": 8, "groups": groups,
+           "groups_on_xcd_L_mod_8": xcd_ok, "us_from_first_group_start": {}}
+    order = [0, 1, 2, 3, 4, 13, 14, 5, 6, 7, 8, 9, 10, 11, 12]
+    for i in order:
+        col = rel[:, i]
+        col = col[~np.isnan(col)]
+        if len(col):
+            out["us_from_first_group_start"][STAMP_NAMES[i]] = {
+                "groups": int(len(col)), "p10": round(float(np.percentile(col, 10)), 2),
+                "median": round(float(np.median(col)), 2),
+                "p90": round(float(np.percentile(col, 90)), 2), "max": round(float(col.max()), 2)}
+    print(json.dumps(out, indent=1))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -394,6 +455,8 @@ def main():
         compute_probe(args.compute_probe, args.diag_lib)
         return
     cfg = CONFIGS[args.config]
+    if args.timeline:
+        return timeline(cfg, args)
     if cfg["kind"] == "step":
         return bench_step(cfg, args)
     layers = max(1, args.layers)

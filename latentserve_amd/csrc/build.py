@@ -2,6 +2,7 @@
 
     python -m latentserve_amd.csrc.build
     python -m latentserve_amd.csrc.build --diagnostics PATH   (measurement build)
+    python -m latentserve_amd.csrc.build --stamps PATH        (timeline build)
 
 Cross-compiles for gfx950 with hipcc; no GPU is needed. Object files go to
 latentserve_amd/csrc/_build/ (git-ignored). The library links the HIP runtime
@@ -50,14 +51,19 @@ def _run(cmd):
     return out
 
 
-def build(verbose: bool = False, diagnostics: bool = False, out: str = LIB) -> str:
+def build(verbose: bool = False, diagnostics: bool = False, out: str = LIB,
+          stamps: bool = False) -> str:
     """Compile and link the library to `out`.  ``diagnostics`` adds
     -DLS_DIAGNOSTICS (ablation variants selected by an environment
-    variable, the page-compute probe): a separate measurement build, never
-    the shipped library."""
+    variable, the page-compute probe); ``stamps`` adds -DLS_STAMPS (each
+    decode workgroup records the clock at numbered points, read back by
+    ls_diag_read_stamps): separate measurement builds, never the shipped
+    library."""
     cc = hipcc()
-    flags = HIP_FLAGS + (["-DLS_DIAGNOSTICS"] if diagnostics else [])
-    obj_dir = os.path.join(HERE, "_build_diag" if diagnostics else "_build")
+    flags = HIP_FLAGS + (["-DLS_DIAGNOSTICS"] if diagnostics else []) + \
+        (["-DLS_STAMPS"] if stamps else [])
+    obj_dir = os.path.join(HERE, "_build_diag" if diagnostics else
+                           "_build_stamps" if stamps else "_build")
     os.makedirs(obj_dir, exist_ok=True)
     objs = [os.path.join(obj_dir, s.replace(".hip", ".o")) for s in SOURCES]
     cmds = [[cc, *flags, "-c", os.path.join(HERE, s), "-o", o] for s, o in zip(SOURCES, objs)]
@@ -75,5 +81,8 @@ if __name__ == "__main__":
     if "--diagnostics" in sys.argv:
         print(build(verbose="-v" in sys.argv, diagnostics=True,
                     out=sys.argv[sys.argv.index("--diagnostics") + 1]))
+    elif "--stamps" in sys.argv:
+        print(build(verbose="-v" in sys.argv, stamps=True,
+                    out=sys.argv[sys.argv.index("--stamps") + 1]))
     else:
         print(build(verbose="-v" in sys.argv))

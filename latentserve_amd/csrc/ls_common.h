@@ -18,6 +18,22 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 constexpr int WAVE = 64;
+
+// Measurement builds only (-DLS_STAMPS, never the shipped library): thread 0
+// of each workgroup records the 100 MHz clock at numbered points of the
+// decode (ls_diag_read_stamps copies the last launch's to the host).
+#ifdef LS_STAMPS
+constexpr int LS_NSTAMP = 16;
+static __device__ uint64_t g_ls_stamps[8192 * LS_NSTAMP];
+#define LS_STAMP(i)                                                                              \
+    do {                                                                                         \
+        if (threadIdx.x == 0)                                                                    \
+            ::ls::g_ls_stamps[(blockIdx.x + gridDim.x * blockIdx.y) * ::ls::LS_NSTAMP + (i)] =   \
+                __builtin_amdgcn_s_memrealtime();                                                \
+    } while (0)
+#else
+#define LS_STAMP(i) do {} while (0)
+#endif
 constexpr int HEAD_DIM = 128;   // the lane mapping below covers exactly 128 channels
 constexpr int PAGE = 16;        // one page = the M=16 side of a 16x16 MFMA tile
 constexpr int MAX_NREP = 16;    // query rows per KV head = the N=16 side of the tile

@@ -706,6 +706,12 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     constexpr int PF_DEPTH = KIND == KV_FP16 ? 2 : 1;
     constexpr int NB = PF_DEPTH + 1;
     __shared__ DecodeSmem<NWT, HG, KIND == KV_INT8> sm;
+    LS_STAMP(0);
+#ifdef LS_STAMPS
+    if (threadIdx.x == 0)           // stamp 15: the XCD this group runs on
+        g_ls_stamps[(blockIdx.x + gridDim.x * blockIdx.y) * LS_NSTAMP + 15] =
+            (uint64_t)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15) | (1ull << 40);
+#endif
     const int H = a.H;
     // A group serves HG adjacent KV heads of one (sequence, split) with NWT
     // waves.  Its work items are (page, head) pairs, claimed one at a time
@@ -926,6 +932,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 const int p_lo = gw.s * per;
                 const int p_hi = p_lo + per < a.score_pages ? p_lo + per : a.score_pages;
                 score_slice<NWT, HG>(a, b, h0, len, p_lo, p_hi);
+                LS_STAMP(1);
                 // the group's score stores complete, then it counts itself in
                 // the word after row (b, h0) (all ones at rest, so the count
                 // reaches Sb - 1 when every group of the sequence is done)
@@ -935,6 +942,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 __syncthreads();
                 if (threadIdx.x == 0)
                     __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                LS_STAMP(2);
                 struct Coop {
                     const DecodeParams& a;
                     int b, h, len, Sb;
@@ -1078,6 +1086,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         if (SPARSE >= 2) {
             fill_table();
             __syncthreads();
+            LS_STAMP(7);
         }
 #pragma unroll
         for (int u = 0; u < PF_DEPTH; ++u)
@@ -1125,6 +1134,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         walk(resolve_lds, first_mem);
     else
         walk(resolve_mem, first_mem);
+    LS_STAMP(8);
 
     const int NR = a.NR;
     const bool single = Sb == 1;
@@ -1219,6 +1229,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             }
         }
     }
+    LS_STAMP(9);
     if (single) return;
 
     // ---- the last group of each (b, h) to arrive merges all splits ----
@@ -1226,6 +1237,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // arrival; the last arriver acquires before reading them.
     handoff_release();
     __syncthreads();
+    LS_STAMP(10);
     if (threadIdx.x < (unsigned)HG) {
         const int64_t bh = (int64_t)b * H + h0 + threadIdx.x;
         const int prev = __hip_atomic_fetch_add(a.counters + bh * COUNTER_STRIDE, 1, __ATOMIC_RELAXED,
@@ -1233,6 +1245,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         sm.is_last[threadIdx.x] = prev == Sb - 1;
     }
     __syncthreads();
+    LS_STAMP(11);
     // a group of HG heads merges each head it closed, 256 threads a head
     const int hh = threadIdx.x / TPH, t256 = threadIdx.x % TPH;
     if (!sm.is_last[hh] || t256 >= 256) return;
@@ -1245,6 +1258,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                             a.out + (int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h, 0, a.so_r,
                             t256);
     }
+    LS_STAMP(12);
     // every group of this (b, h) has arrived: back to zero for the next launch
     if (t256 == 0)
         __hip_atomic_store(a.counters + bh * COUNTER_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1270,6 +1284,13 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
                                                (p.out_f32 ? 4 : 2),
                             p.out_f32, p.so_r, threadIdx.x);
 }
+
+#ifdef LS_STAMPS
+// Measurement build: the stamps of the last launch, copied to the host.
+extern "C" int ls_diag_read_stamps(void* host, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_ls_stamps), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
 
 // ------------------------------------------------------------- launch ----
 

@@ -114,6 +114,7 @@ __device__ __attribute__((always_inline)) void select_keys(const float* srow, in
     const int last = P > 0 ? P - 1 : 0;
     if constexpr (COOP) {
         fix.wait();             // until the row's writers say they are done
+        LS_STAMP(3);
 #pragma unroll
         for (int j = 0; j < KPT; ++j)
             f[j] = P > 0 ? load_coherent(srow + (i0 + j < last ? i0 + j : last)) : 0.f;
@@ -142,6 +143,7 @@ __device__ __attribute__((always_inline)) void select_keys(const float* srow, in
             }
             __builtin_amdgcn_s_sleep(2);
         }
+        LS_STAMP(4);
     } else {
 #pragma unroll
         for (int j = 0; j < KPT; ++j) f[j] = P > 0 ? srow[i0 + j < last ? i0 + j : last] : 0.f;
@@ -472,6 +474,7 @@ __device__ __attribute__((always_inline)) void select_row_lin(const float* srow,
             sm.red[par][1][wv] = kmx;
         }
         __syncthreads();
+        if (par == 0) LS_STAMP(13);
         // (the other parity's histogram and vote were last read before this
         // barrier)
         if (tid == 0) vote[par ^ 1] = 0;
@@ -497,6 +500,7 @@ __device__ __attribute__((always_inline)) void select_row_lin(const float* srow,
             atomicAdd(&sm.hist[par][((cm >> j) & 1u) ? (int)b : spare], 1u);
         }
         __syncthreads();
+        if (par == 0) LS_STAMP(14);
         // this thread's bins, highest first: 2047 - 8 tid - j
         const u4 b_lo = *(const u4*)&sm.hist[par][LIN_BINS - 8 - tid * BPT];
         const u4 b_hi = *(const u4*)&sm.hist[par][LIN_BINS - 4 - tid * BPT];
@@ -559,6 +563,7 @@ __device__ __attribute__((always_inline)) void select_row_lin(const float* srow,
         }
         if (!more) break;
     }
+    LS_STAMP(5);
     uint32_t am = 0u, cm = 0u;          // keys above; candidates
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
@@ -634,6 +639,7 @@ __device__ __attribute__((always_inline)) void select_row_lin(const float* srow,
 #pragma unroll
     for (int j = 0; j < KPT; ++j)
         if ((take >> j) & 1u) emit(pos++, i0 + j);
+    LS_STAMP(6);
 }
 
 template <bool SORTED, class Emit>
