@@ -90,8 +90,8 @@ class CapturedDecode:
         self.ids = torch.zeros(batch_size, 1, dtype=torch.long, device=dev)
         self.positions = torch.zeros(batch_size, 1, dtype=torch.long, device=dev)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
-        self.static_logits: Optional[torch.Tensor] = None
-        self.static_next: Optional[torch.Tensor] = None
+        self.logits_buf: Optional[torch.Tensor] = None
+        self.next_buf: Optional[torch.Tensor] = None
         self.replays = 0
 
     def _forward(self):
@@ -117,13 +117,13 @@ class CapturedDecode:
             torch.cuda.current_stream().wait_stream(side)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, pool=pool):
-                self.static_logits, self.static_next = self._forward()
+                self.logits_buf, self.next_buf = self._forward()
         self.graph = g
 
     def replay(self) -> torch.Tensor:
         self.graph.replay()
         self.replays += 1
-        return self.static_logits
+        return self.logits_buf
 
 
 class GraphedDecoder:
@@ -235,7 +235,7 @@ class GraphedDecoder:
             raise RuntimeError("greedy steps need GraphedDecoder(..., greedy=True)")
         logits = self.step(token_ids, positions, slots)
         if self._last_graph is not None:
-            return self._last_graph.static_next
+            return self._last_graph.next_buf
         return fe.argmax_rows(logits[:, -1, :])
 
     def stats(self) -> dict:

@@ -122,7 +122,7 @@ def test_greedy_step_is_the_captured_argmax():
     for t in range(5):
         pos = torch.full((2, 1), t, dtype=torch.long, device="cuda")
         nxt = dec.step_greedy(tok, pos, slots=[0, 1])
-        logits = dec._last_graph.static_logits
+        logits = dec._last_graph.logits_buf
         assert torch.equal(nxt, logits[:, -1].argmax(-1, keepdim=True))
         tok = nxt.clone()
 
