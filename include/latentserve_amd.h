@@ -198,11 +198,11 @@ int ls_page_scores(const void* q, const int64_t* q_strides, const void* kmin, co
  * bound_strides (block, head); page 0 and the last `recent` pages +inf,
  * pages past the end -inf), exchanged through `scores` fp32 [B, H_kv,
  * >= max_pages + 1] (the word after a row counts the workgroups that have
- * stored their share; every byte 0xFF before the first call, and every call
- * leaves it so), then each workgroup selects and attends as
- * ls_sparse_attention_fp16 does.  A share that has not arrived after 50 us
- * is computed by the reader itself, so no workgroup depends on another
- * being resident.
+ * stored their share: all ones before the first call, and every call leaves
+ * it so; the rows keep the last call's scores), then each workgroup selects
+ * and attends as ls_sparse_attention_fp16 does.  A workgroup that does not
+ * see every share stored within 50 us computes the scores it needs itself,
+ * so no workgroup depends on another being resident.
  * Replaces the index + select + attend steps of sparse_attention
  * (kernels/cuda/paged_sparse.py:222-251; page_index, paged_sparse_fp16.cu:
  * 78-130).  k <= max_pages <= 2048 (COOP_MAX_PAGES), n_rep <= 8

@@ -948,13 +948,17 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                     int b, h, len, Sb;
                     const int* done;
                     __device__ float operator()(int p) const { return score_one(a, b, h, len, p); }
-                    __device__ uint64_t ticks() const { return a.coop_wait_ticks; }
-                    __device__ void wait() const {
-                        // one word polled (every thread of a wave reads the same line)
+                    // true once every group of the sequence has counted itself
+                    // (one word polled: every thread of a wave reads the same
+                    // line), false if that does not happen within the bound
+                    __device__ bool wait() const {
                         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-                        while (load_coherent(done) != Sb - 1 &&
-                               __builtin_amdgcn_s_memrealtime() - t0 < a.coop_wait_ticks)
+                        while (true) {
+                            if (load_coherent(done) == Sb - 1) return true;
+                            if (__builtin_amdgcn_s_memrealtime() - t0 >= a.coop_wait_ticks)
+                                return false;
                             __builtin_amdgcn_s_sleep(8);
+                        }
                     }
                 };
                 const Coop fix{a, b, h0 + hh, len, Sb, done};
@@ -969,13 +973,13 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                                        emit);
             }
             __syncthreads();
-            if (SPARSE == 3 && Sb == 1) {
-                // the only reader of its rows: back to all ones (with the
-                // count after row (b, h0))
-                for (int p = tid; p <= a.score_pages; p += 256)
-                    __hip_atomic_store((uint32_t*)(a.scores + (int64_t)b * a.ssc_b +
-                                                   (int64_t)(h0 + hh) * a.ssc_h + p),
-                                       EMPTY_WORD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (SPARSE == 3 && Sb == 1 && threadIdx.x == 0) {
+                // the only reader of its rows: the count after row (b, h0)
+                // back to all ones (the rows keep their scores: a call reads
+                // them only after its writers counted themselves)
+                __hip_atomic_store((uint32_t*)(a.scores + (int64_t)b * a.ssc_b +
+                                               (int64_t)h0 * a.ssc_h + a.score_pages),
+                                   EMPTY_WORD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             const int32_t* trow = a.block_tables + (int64_t)b * a.sbt_b;
             for (int i = threadIdx.x; i < n_ent * HG; i += WAVE * NWT) {
@@ -1263,11 +1267,13 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     if (t256 == 0)
         __hip_atomic_store(a.counters + bh * COUNTER_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if constexpr (SPARSE == 3) {
-        // and every group has read this row's scores: back to all ones (with
-        // the count after row (b, h0))
-        for (int p = t256; p <= a.score_pages; p += 256)
+        // and every group has read the count after row (b, h0) (a group
+        // counts itself before it selects, and arrives here after): back to
+        // all ones.  Every group serves all HG heads and arrives for them
+        // together, so head h0's last arriver comes after all of them.
+        if (t256 == 0 && hh == 0)
             __hip_atomic_store((uint32_t*)(a.scores + (int64_t)b * a.ssc_b +
-                                           (int64_t)(h0 + hh) * a.ssc_h + p),
+                                           (int64_t)h0 * a.ssc_h + a.score_pages),
                                EMPTY_WORD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }

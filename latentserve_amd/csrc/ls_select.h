@@ -90,16 +90,15 @@ __device__ __forceinline__ uint32_t group_scan(uint32_t v, uint32_t* wsum, int t
 // one group a head): three a radix pass, one a scan after them.
 //
 // COOP: the row is being written by other workgroups of the same launch
-// (the selecting decode's own scoring): after `fix.wait()` (the writers'
-// count, bounded in time) it is read with device-coherent loads, a word
-// still all ones (EMPTY_WORD, never a score) is read again until it lands,
-// and after `fix.ticks()` of the 100 MHz clock the missing scores are
-// computed by `fix(page)` instead (the same bits: the writers compute them
-// the same way), so no workgroup depends on another being resident.
+// (the selecting decode's own scoring): once `fix.wait()` reports the
+// writers' count complete it is read with device-coherent loads; if the
+// count does not complete within its time bound, every score the thread
+// needs is computed by `fix(page)` instead (the same bits: the writers
+// compute them the same way, and the row may still hold an earlier call's
+// scores), so no workgroup depends on another being resident.
 struct NoFix {
     __device__ float operator()(int) const { return 0.f; }
-    __device__ void wait() const {}
-    __device__ uint64_t ticks() const { return 0; }
+    __device__ bool wait() const { return true; }
 };
 
 // A thread's KPT keys of the row (pages tid * KPT ...), as order keys;
@@ -113,35 +112,17 @@ __device__ __attribute__((always_inline)) void select_keys(const float* srow, in
     float f[KPT];
     const int last = P > 0 ? P - 1 : 0;
     if constexpr (COOP) {
-        fix.wait();             // until the row's writers say they are done
+        const bool done = fix.wait();   // the row's writers say they are done
         LS_STAMP(3);
-#pragma unroll
-        for (int j = 0; j < KPT; ++j)
-            f[j] = P > 0 ? load_coherent(srow + (i0 + j < last ? i0 + j : last)) : 0.f;
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        while (true) {
-            bool missing = false;
+        if (done) {
 #pragma unroll
             for (int j = 0; j < KPT; ++j)
-                missing = missing || (j < cnt && __builtin_bit_cast(uint32_t, f[j]) == EMPTY_WORD);
-            if (!missing) break;
-            // a round reads all of the thread's keys again, unconditionally:
-            // loads under per-key branches would each wait for the last
-            float g[KPT];
+                f[j] = P > 0 ? load_coherent(srow + (i0 + j < last ? i0 + j : last)) : 0.f;
+        } else {
+            // a writer not seen finishing in time: this thread's scores
+            // computed here, none read from the row
 #pragma unroll
-            for (int j = 0; j < KPT; ++j)
-                g[j] = load_coherent(srow + (i0 + j < last ? i0 + j : last));
-#pragma unroll
-            for (int j = 0; j < KPT; ++j)
-                f[j] = __builtin_bit_cast(uint32_t, f[j]) == EMPTY_WORD ? g[j] : f[j];
-            if (__builtin_amdgcn_s_memrealtime() - t0 > fix.ticks()) {
-#pragma unroll
-                for (int j = 0; j < KPT; ++j)
-                    if (j < cnt && __builtin_bit_cast(uint32_t, f[j]) == EMPTY_WORD)
-                        f[j] = fix(i0 + j);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
+            for (int j = 0; j < KPT; ++j) f[j] = j < cnt ? fix(i0 + j) : 0.f;
         }
         LS_STAMP(4);
     } else {

@@ -304,7 +304,8 @@ def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
     if (scoring == "bounds" and block_tables.shape[1] <= COOP_MAX_PAGES
             and n_rep <= COOP_MAX_NREP):
         # one launch: the decode's workgroups score the pages themselves,
-        # exchanging the scores through a buffer kept all ones at rest
+        # exchanging the scores through a buffer whose count words are all
+        # ones at rest
         _check_bounds(kmin, kmax, q.device)
         # (each row is followed by one word: the count of its scored shares)
         ws = scratch("sparse_coop_scores", (b, h, block_tables.shape[1] + 1), torch.int32,
