@@ -132,7 +132,8 @@ __device__ __forceinline__ _Float16 rope_h(_Float16 x, _Float16 c, _Float16 y, _
 // B16 x 16K decode (49.6 -> 65.5 us).  Only stores made write-through may
 // be handed off this way.
 // Acquire side: the last arriver reads the partials with device-coherent
-// loads (sc1, relaxed agent-scope atomic loads), issued after its RMW has
+// loads (sc1: relaxed agent-scope atomic loads of up to 8 bytes, 16-byte
+// buffer loads with the sc1 policy), issued after its RMW has
 // returned the final count (the branch on it orders them), so no line can
 // come from a stale copy in its XCD's L2.  The model's agent-scope acquire
 // fence (an invalidate of the reader's whole L2) measured +2.1 us a launch
@@ -146,21 +147,20 @@ __device__ __forceinline__ T load_coherent(const T* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Sixteen bytes the same way (a global_load_dwordx4 with sc1).  The
-// compiler does not track an asm load: the caller issues its loads, then
-// coherent_wait() on every value loaded before using any of them.
-__device__ __forceinline__ f4 load_coherent4_issue(const float* p) {
-    f4 v;
-    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
-    return v;
+// Sixteen bytes the same way: a raw buffer load with the sc1 cache policy
+// (buffer_load_dwordx4 ... sc1), from a resource over `base` (offsets in
+// bytes, below 2^31).  A builtin, so the compiler inserts the wait before
+// any use of the value, as for the atomic loads above.  (An inline-asm load
+// is not tracked: with an explicit wait after it the compiler still took
+// the asm's outputs as ready at once, and reading m and l of the records
+// that way gave wrong results.)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const float* base) {
+    // (dword 3: the raw-buffer format bits CDNA's buffer instructions expect)
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, 0x7fffffff, 0x00020000);
 }
-__device__ __forceinline__ void coherent_wait() {
-    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
-}
-// Ties a value to the wait above it: later uses read the register after it.
-template <class T>
-__device__ __forceinline__ void coherent_pin(T& v) {
-    asm volatile("" : "+v"(v));
+__device__ __forceinline__ f4 load_coherent4(__amdgpu_buffer_rsrc_t rs, int byte_off) {
+    constexpr int SC1 = 16;             // the cache-policy operand's sc1 bit
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, SC1));
 }
 
 // Workgroup ids renumbered XCD-major.  The dispatcher deals a launch's

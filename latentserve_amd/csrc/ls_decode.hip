@@ -332,8 +332,17 @@ __device__ __forceinline__ void store_coherent4(float* p, f4 v) {
     asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
 
-// VEC 4: 16-byte loads; 1: scalar loads; 0: device-coherent scalar loads
-// (partials written by other workgroups of the same launch).
+// Eight bytes the same way.
+__device__ __forceinline__ void store_coherent2(float* p, float x, float y) {
+    u2 v;
+    v.x = __builtin_bit_cast(uint32_t, x);
+    v.y = __builtin_bit_cast(uint32_t, y);
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// VEC 4: 16-byte loads; 1: scalar loads; 0: device-coherent loads of the
+// fused decode's records (written by other workgroups of the same launch;
+// m and l of a row side by side at m + 2 r, `l` unused).
 template <int VEC>
 __device__ void combine_partials(const float* acc, const float* m, const float* l, int S, int NR,
                                  int64_t sa_s, int64_t sa_r, int64_t sm_s, void* out, int out_f32,
@@ -342,10 +351,14 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
         const int r = o / (HEAD_DIM / 4), d0 = (o % (HEAD_DIM / 4)) * 4;
         float mg = neg_inf(), lt = 0.f;
         float at[4] = {0.f, 0.f, 0.f, 0.f};
+        // VEC 0: the records through a buffer resource, so the 16-byte
+        // device-coherent (sc1) loads are ones the compiler waits for
+        const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(acc);
         for (int s0 = 0; s0 < S; s0 += CMB_CHUNK) {
             const int n = S - s0 < CMB_CHUNK ? S - s0 : CMB_CHUNK;
             float mv[CMB_CHUNK], lv[CMB_CHUNK], av[CMB_CHUNK][4];
             f4 avc[CMB_CHUNK];
+            uint64_t mlc[CMB_CHUNK];
             // Every slot loads (slots past the last split reread it) and is
             // masked afterwards: loads under a branch would each wait for
             // the one before.
@@ -354,9 +367,11 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
                 const int64_t sp = s0 + i < S ? s0 + i : S - 1;
                 const float* src = acc + sp * sa_s + r * sa_r + d0;
                 if (VEC == 0) {
-                    mv[i] = load_coherent(m + sp * sm_s + r);
-                    lv[i] = load_coherent(l + sp * sm_s + r);
-                    avc[i] = load_coherent4_issue(src);
+                    // (m and l as one relaxed 8-byte atomic load: sc1, and
+                    // the compiler tracks its wait)
+                    mlc[i] = __hip_atomic_load((const uint64_t*)(m + sp * sm_s + 2 * r),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    avc[i] = load_coherent4(rs, (int)((src - acc) * sizeof(float)));
                     continue;
                 }
                 mv[i] = m[sp * sm_s + r];
@@ -371,12 +386,12 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
                 }
             }
             if (VEC == 0) {
-                coherent_wait();
 #pragma unroll
                 for (int i = 0; i < CMB_CHUNK; ++i) {
-                    coherent_pin(avc[i]);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) av[i][e] = avc[i][e];
+                    mv[i] = __builtin_bit_cast(float, (uint32_t)mlc[i]);
+                    lv[i] = __builtin_bit_cast(float, (uint32_t)(mlc[i] >> 32));
                 }
             }
 #pragma unroll
@@ -1194,8 +1209,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         const int hh = threadIdx.x / TPH, t256 = threadIdx.x % TPH;
         const int d0 = (t256 % 32) * 4;
         float* pacc = a.work + ((int64_t)w_rec * H + h0 + hh) * rec;
-        float* pm = pacc + NR * HEAD_DIM;
-        float* pl = pm + MAX_NREP;
+        float* pm = pacc + NR * HEAD_DIM;       // (m, l) of each row
         for (int r = t256 / 32; r < NR; r += TPH / 32) {
             float mv[NWH], lv[NWH];
             f4 av[NWH];
@@ -1229,8 +1243,10 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 // one's.
                 store_coherent4(pacc + r * HEAD_DIM + d0, at);
                 if (d0 == 0) {
-                    store_coherent(pm + r, mg * LN2);   // natural-log units, the reference's format
-                    store_coherent(pl + r, lt);
+                    // (m in natural-log units, the reference's format; m and l
+                    // of a row side by side: the combining group reads them
+                    // as one 8-byte load)
+                    store_coherent2(pm + 2 * r, mg * LN2, lt);
                 }
             }
         }
@@ -1259,7 +1275,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     {
         // device-coherent loads: the records of groups on other XCDs
         const float* recs = a.work + ((int64_t)gw.first * H + h0 + hh) * rec;
-        combine_partials<0>(recs, recs + NR * HEAD_DIM, recs + NR * HEAD_DIM + MAX_NREP, Sb, NR,
+        combine_partials<0>(recs, recs + NR * HEAD_DIM, nullptr, Sb, NR,
                             (int64_t)H * rec, HEAD_DIM, (int64_t)H * rec,
                             a.out + (int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h, 0, a.so_r,
                             t256);
