@@ -385,7 +385,7 @@ def compute_probe(items, diag_lib):
 
 # The decode's stamp points (csrc/ls_decode.hip, ls_select.h; LS_STAMP).
 STAMP_NAMES = {0: "group start", 1: "own share scored", 2: "scores released, counted",
-               3: "peers' count seen", 4: "row keys loaded", 13: "extrema barrier",
+               3: "peers' count seen", 4: "row keys requested", 13: "extrema barrier",
                14: "histogram barrier", 5: "threshold search done", 6: "list emitted",
                7: "walk start", 8: "wave 0 walk end", 9: "waves merged, records stored",
                10: "records released", 11: "arrival counted", 12: "combine done"}
