@@ -36,11 +36,12 @@
 //  * Page prefetch: the next page's K/V (and scales) are issued before the
 //    current page is computed (two register buffers).
 //  * Splits: NW waves merge in LDS; with more than one split, every group
-//    writes (m, l, acc) partials in the reference's layout ([B,H,S,NR,D],
-//    [B,H,S,NR], m in natural-log units) and the last group to finish a
-//    (sequence, head) merges them (combine_splits, paged_decode.py:689-706)
-//    and resets its arrival counter, so the path is one launch and safe to
-//    replay in a captured graph.
+//    writes its (acc, m, l) record (acc [NR][128] as the reference's
+//    partials hold it, then each row's m, in natural-log units as the
+//    reference's, beside its l) and the last group to finish a (sequence,
+//    head) merges them (combine_splits, paged_decode.py:689-706) and resets
+//    its arrival counter, so the path is one launch and safe to replay in a
+//    captured graph.
 
 #include <stdlib.h>
 #include <string.h>
