@@ -104,20 +104,26 @@ struct PageBuf {
 template <int KIND, bool ASYM, bool HAS_RES>
 __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, int blk, int page,
                                           int num_pages, int res_row, int h, int g, int c) {
+    // (blk and h are the same in every lane: the wave's item)
     const int64_t base = (int64_t)blk * a.sk_b + (int64_t)h * a.sk_h;
     if (KIND == KV_FP16) {
-        const half_t* kp = (const half_t*)a.k_pool + base + (int64_t)c * a.sk_p + 8 * g;
-        const half_t* vp = (const half_t*)a.v_pool + base + (int64_t)(4 * g) * a.sk_p + 8 * c;
+        const __amdgpu_buffer_rsrc_t rk = page_rsrc((const half_t*)a.k_pool + base);
+        const __amdgpu_buffer_rsrc_t rv = page_rsrc((const half_t*)a.v_pool + base);
+        const int ko = (int)(((int64_t)c * a.sk_p + 8 * g) * sizeof(half_t));
+        const int vo = (int)(((int64_t)(4 * g) * a.sk_p + 8 * c) * sizeof(half_t));
+        const int row = (int)(a.sk_p * sizeof(half_t));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) buf.k[j] = stream_load((const u4*)(kp + 32 * j));
+        for (int j = 0; j < 4; ++j) buf.k[j] = page_load16(rk, ko + 64 * j);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) buf.v[i] = stream_load((const u4*)(vp + (int64_t)i * a.sk_p));
+        for (int i = 0; i < 4; ++i) buf.v[i] = page_load16(rv, vo + i * row);
     } else {
         buf.res = HAS_RES && page == num_pages - 1;
-        const int8_t* vp = (const int8_t*)a.v_pool + base + (int64_t)(4 * g) * a.sk_p + 8 * c;
+        const __amdgpu_buffer_rsrc_t rv = page_rsrc((const int8_t*)a.v_pool + base);
+        const int vo = (int)((int64_t)(4 * g) * a.sk_p + 8 * c);
+        const int row = (int)a.sk_p;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const u2 t = stream_load((const u2*)(vp + (int64_t)i * a.sk_p));
+            const u2 t = page_load8(rv, vo + i * row);
             buf.v[i].x = t.x;
             buf.v[i].y = t.y;
         }
@@ -137,9 +143,10 @@ __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, i
 #pragma unroll
             for (int j = 0; j < 4; ++j) buf.k[j] = *(const u4*)(kp + 64 * (j / 2) + 8 * (j % 2));
         } else {
-            const int8_t* kp = (const int8_t*)a.k_pool + base + (int64_t)c * a.sk_p + 16 * g;
+            const __amdgpu_buffer_rsrc_t rk = page_rsrc((const int8_t*)a.k_pool + base);
+            const int ko = (int)((int64_t)c * a.sk_p + 16 * g);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) buf.k[j] = stream_load((const u4*)(kp + 64 * j));
+            for (int j = 0; j < 2; ++j) buf.k[j] = page_load16(rk, ko + 64 * j);
             // One coalesced 512-byte row per page, 8 bytes a lane; the
             // compute step spreads it through LDS to the lanes that need
             // each channel (16 lanes share every scale).
