@@ -116,6 +116,9 @@ constexpr int PAGE_POLICY = 1 /* sc0 */ | 2 /* nt */;
 __device__ __forceinline__ u4 page_load16(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, PAGE_POLICY));
 }
+__device__ __forceinline__ float page_load4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, PAGE_POLICY));
+}
 __device__ __forceinline__ u2 page_load8(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, PAGE_POLICY));
 }

@@ -75,8 +75,8 @@ __global__ __launch_bounds__(256) void page_index_kernel(IndexParams a) {
             } else {
                 st[i] = PG_SCORE;
                 const int64_t off = (int64_t)blk * a.sb_b + (int64_t)h * a.sb_h + c0;
-                lo[i] = *(const u4*)((const half_t*)a.kmin + off);
-                hi[i] = *(const u4*)((const half_t*)a.kmax + off);
+                lo[i] = stream_load((const u4*)((const half_t*)a.kmin + off));
+                hi[i] = stream_load((const u4*)((const half_t*)a.kmax + off));
             }
         }
     }
