@@ -174,7 +174,7 @@ __device__ __forceinline__ T load_coherent(const T* p) {
 }
 
 // Sixteen bytes the same way: a raw buffer load with the sc1 cache policy
-// (buffer_load_dwordx4 ... sc1), from a resource over `base` (offsets in
+// (buffer_load_dwordx4 ... sc1 nt), from a resource over `base` (offsets in
 // bytes, below 2^31).  A builtin, so the compiler inserts the wait before
 // any use of the value, as for the atomic loads above.  (An inline-asm load
 // is not tracked: with an explicit wait after it the compiler still took
@@ -185,8 +185,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const float* bas
     return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, 0x7fffffff, 0x00020000);
 }
 __device__ __forceinline__ f4 load_coherent4(__amdgpu_buffer_rsrc_t rs, int byte_off) {
-    constexpr int SC1 = 16;             // the cache-policy operand's sc1 bit
-    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, SC1));
+    // the cache-policy operand: sc1 (device coherent) | nt (each record is
+    // read once: 0.05 us faster at B16 x 16K than sc1 alone)
+    constexpr int POLICY = 16 | 2;
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, POLICY));
 }
 
 // Workgroup ids renumbered XCD-major.  The dispatcher deals a launch's
