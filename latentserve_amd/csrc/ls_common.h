@@ -105,17 +105,29 @@ __device__ __forceinline__ T stream_load(const T* p) {
 // (B16 x 16K, one box, alternating): 48.87 -> 48.56 us (buffer loads with
 // the nontemporal policy alone 48.65; sc1 with it 48.57; sc1 alone 54.2;
 // plain loads 52.7).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const void* wave_uniform_base) {
+// `fetch` false (the same in every lane): a resource of no bytes, whose
+// loads return zeros without a memory request (the walk's requests for
+// items past its end, which the compute masks).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const void* wave_uniform_base,
+                                                            bool fetch = true) {
     const uint64_t x = (uint64_t)wave_uniform_base;
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
-    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), 0, 0x7fffffff,
-                                             0x00020000);
+    const int n = __builtin_amdgcn_readfirstlane(fetch ? 0x7fffffff : 0);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), 0, n, 0x00020000);
 }
 constexpr int PAGE_POLICY = 1 /* sc0 */ | 2 /* nt */;
 __device__ __forceinline__ u4 page_load16(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, PAGE_POLICY));
 }
+// A scheduling barrier after each of an fp16 page's loads: the loads go out
+// where the walk issues them, in order.  Left to the scheduler, they were
+// moved among the compute of the page before (B16 x 16K: 48.46 -> 47.15 us
+// with the barriers; an s_nop after each load, which also pins them,
+// 47.51).  The INT8 walk is faster without them (B16 x 16K: 33.37 against
+// 34.13 us).
+__device__ __forceinline__ void issue_here() { __builtin_amdgcn_sched_barrier(0); }
+
 __device__ __forceinline__ float page_load4(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, PAGE_POLICY));
 }

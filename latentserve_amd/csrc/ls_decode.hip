@@ -103,22 +103,29 @@ struct PageBuf {
 
 template <int KIND, bool ASYM, bool HAS_RES>
 __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, int blk, int page,
-                                          int num_pages, int res_row, int h, int g, int c) {
+                                          int num_pages, int res_row, int h, int g, int c,
+                                          bool fetch = true) {
     // (blk and h are the same in every lane: the wave's item)
     const int64_t base = (int64_t)blk * a.sk_b + (int64_t)h * a.sk_h;
     if (KIND == KV_FP16) {
-        const __amdgpu_buffer_rsrc_t rk = page_rsrc((const half_t*)a.k_pool + base);
-        const __amdgpu_buffer_rsrc_t rv = page_rsrc((const half_t*)a.v_pool + base);
+        const __amdgpu_buffer_rsrc_t rk = page_rsrc((const half_t*)a.k_pool + base, fetch);
+        const __amdgpu_buffer_rsrc_t rv = page_rsrc((const half_t*)a.v_pool + base, fetch);
         const int ko = (int)(((int64_t)c * a.sk_p + 8 * g) * sizeof(half_t));
         const int vo = (int)(((int64_t)(4 * g) * a.sk_p + 8 * c) * sizeof(half_t));
         const int row = (int)(a.sk_p * sizeof(half_t));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) buf.k[j] = page_load16(rk, ko + 64 * j);
+        for (int j = 0; j < 4; ++j) {
+            buf.k[j] = page_load16(rk, ko + 64 * j);
+            issue_here();
+        }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) buf.v[i] = page_load16(rv, vo + i * row);
+        for (int i = 0; i < 4; ++i) {
+            buf.v[i] = page_load16(rv, vo + i * row);
+            issue_here();
+        }
     } else {
         buf.res = HAS_RES && page == num_pages - 1;
-        const __amdgpu_buffer_rsrc_t rv = page_rsrc((const int8_t*)a.v_pool + base);
+        const __amdgpu_buffer_rsrc_t rv = page_rsrc((const int8_t*)a.v_pool + base, fetch);
         const int vo = (int)((int64_t)(4 * g) * a.sk_p + 8 * c);
         const int row = (int)a.sk_p;
 #pragma unroll
@@ -134,8 +141,8 @@ __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, i
         // B16 x 16K)
         const int64_t vsb = (int64_t)blk * a.svs_b + (int64_t)h * a.svs_h;
         const int vso = (int)(c * a.svs_p * (int64_t)sizeof(float));
-        buf.vs = page_load4(page_rsrc(a.v_scale + vsb), vso);
-        if (ASYM) buf.vz = page_load4(page_rsrc(a.v_zero + vsb), vso);
+        buf.vs = page_load4(page_rsrc(a.v_scale + vsb, fetch), vso);
+        if (ASYM) buf.vz = page_load4(page_rsrc(a.v_zero + vsb, fetch), vso);
         // K channels in the INT8 order: lane (c, g) takes 16 contiguous
         // channels 64j+16g.. of token c per load, so one load instruction
         // covers 64 bytes of each of 16 token rows (8 bytes a lane would
@@ -147,19 +154,21 @@ __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, i
 #pragma unroll
             for (int j = 0; j < 4; ++j) buf.k[j] = *(const u4*)(kp + 64 * (j / 2) + 8 * (j % 2));
         } else {
-            const __amdgpu_buffer_rsrc_t rk = page_rsrc((const int8_t*)a.k_pool + base);
+            const __amdgpu_buffer_rsrc_t rk = page_rsrc((const int8_t*)a.k_pool + base, fetch);
             const int ko = (int)((int64_t)c * a.sk_p + 16 * g);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) buf.k[j] = page_load16(rk, ko + 64 * j);
+            for (int j = 0; j < 2; ++j) {
+                buf.k[j] = page_load16(rk, ko + 64 * j);
+            }
             // One coalesced 512-byte row per page, 8 bytes a lane; the
             // compute step spreads it through LDS to the lanes that need
             // each channel (16 lanes share every scale).
             const int lane = 16 * g + c;
             const float* ksp = a.k_scale + (int64_t)blk * a.sks_b + (int64_t)h * a.sks_h;
-            buf.ks = page_load8(page_rsrc(ksp), 8 * lane);
+            buf.ks = page_load8(page_rsrc(ksp, fetch), 8 * lane);
             if (ASYM) {
                 const float* kzp = a.k_zero + (int64_t)blk * a.sks_b + (int64_t)h * a.sks_h;
-                buf.kz = page_load8(page_rsrc(kzp), 8 * lane);
+                buf.kz = page_load8(page_rsrc(kzp, fetch), 8 * lane);
             }
         }
     }
@@ -838,9 +847,14 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         // A request needs only a block id that is safe to read: the item is
         // checked against the sequence when it is computed (and the walk
         // never holds an INT8 sequence's residual page: it is computed apart)
-        const int safe_blk = (unsigned)blk < (unsigned)a.num_blocks ? blk : 0;
+        // (an item with no block, past the end included, is requested from a
+        // resource of no bytes at block 0's address: zeros, no memory
+        // request)
+        const bool valid = (unsigned)blk < (unsigned)a.num_blocks;
+        const int safe_blk = valid ? blk : 0;
+        const bool fetch = valid;
         load_page<KIND, ASYM, KIND == KV_FP16 && HAS_RES>(a, buf[slot], safe_blk, -1, 0, 0,
-                                                          h0 + hw, g, c);
+                                                          h0 + hw, g, c, fetch);
     };
     // Which sequence and split this group serves: the host grid's for a
     // page-subset walk, else the length-proportional deal.
