@@ -654,6 +654,8 @@ __device__ void score_slice(const DecodeParams& a, int b, int h0, int len, int p
             st[r] = p >= p_hi ? 0 : p >= np ? 3 : (p == 0 || p >= np - a.recent) ? 2 : 1;
             const int pc = p < a.max_pages ? p : a.max_pages - 1;
             blk[r] = a.block_tables[(int64_t)b * a.sbt_b + pc];
+            issue_here();   // the table and bounds loads go out where written,
+                            // in order (B8 x 32K: 45.77 -> 45.44 us)
         }
         u4 lo[R], hi[R];
 #pragma unroll
@@ -665,6 +667,7 @@ __device__ void score_slice(const DecodeParams& a, int b, int h0, int len, int p
             // than plain loads)
             lo[r] = stream_load((const u4*)((const half_t*)a.kmin + off));
             hi[r] = stream_load((const u4*)((const half_t*)a.kmax + off));
+            issue_here();
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
