@@ -10,7 +10,8 @@ graph and the graph is replayed, timed with HIP events on the launch stream.
 
 Configs: c1 B1x2048, c2 B16x16384 (the headline), c3
 B8x32768, c3r ragged B16 with lengths ~U[512, 32768], c4 INT8 B16x16384,
-c5 sparse (50% of pages, selected on the GPU each step) B8x32768.
+c5 sparse (50% of pages, selected on the GPU each step) B8x32768, c5h the
+same at B16x16384.
 Inputs are synthetic N(0,1) fp16 from a seeded device generator; block
 tables are a seeded permutation of the pool (non-contiguous pages).
 
@@ -42,6 +43,8 @@ CONFIGS = {
                 workload="fp16 paged decode B16 ragged L~U[512,32768]"),
     # diagnostic: the same bytes as c2 in 512 short sequences (no split merge needed)
     "flat": dict(batch=512, ctx=512, kind="fp16", workload="fp16 paged decode B512 x 512"),
+    # diagnostic: the attention shape of the full step (B16 x 8K) on its own
+    "s8k": dict(batch=16, ctx=8192, kind="fp16", workload="fp16 paged decode B16 x 8192"),
     "c4": dict(batch=16, ctx=16384, kind="int8",
                workload="INT8 paged decode B16 x 16384 (fp32 scales, fp16 last-page K residual)"),
     # BASELINE configuration 5, second part: a whole decode step of the
@@ -52,6 +55,10 @@ CONFIGS = {
     "c5": dict(batch=8, ctx=32768, kind="sparse", ratio=0.5,
                workload="sparse 50% paged decode B8 x 32768 (page index + top-k + page-subset "
                         "attention)"),
+    # the sparse variant at the headline shape
+    "c5h": dict(batch=16, ctx=16384, kind="sparse", ratio=0.5,
+                workload="sparse 50% paged decode B16 x 16384 (page index + top-k + page-subset "
+                         "attention)"),
 }
 
 

@@ -15,10 +15,11 @@ permutation of the pool; the C oracle runs on the host's cores (OpenMP).
   ls_int8_finalize_blocks (K) and ls_int8_decode_write (V), codes and scales
   bit-exact against the oracle's quantizers, the last page of K in the fp16
   residual, output against the oracle over the INT8 cache.
-* C5 sparse 50 % B8 x 32768: page bounds bit-exact, page scores against the
-  oracle, the GPU selection as sets against the oracle's stable top-k (swaps
-  allowed only inside score near-ties), outputs of the list decode and of
-  the selecting decode against the oracle's sparse_decode.
+* C5 sparse 50 % B8 x 32768, and C5h the same at the headline B16 x 16384:
+  page bounds bit-exact, page scores against the oracle, the GPU selection
+  as sets against the oracle's stable top-k (swaps allowed only inside
+  score near-ties), outputs of the list decode and of the selecting decode
+  against the oracle's sparse_decode.
 
 The reference's GPU tests take the same shape of check at smaller sizes
 (tests/test_cuda_decode.py:82-91, tests/test_phase14_sparse_kernels.py:92-134).
@@ -176,11 +177,13 @@ def _sets_agree(got_sel, want_sel, scores, what):
                     f"{what}: b={i} h={j} page {p} (score {row[p]}, k-th {kth})"
 
 
-def test_c5_sparse_half_b8x32k():
+def _sparse_half_at_full_size(batch, ctx, seed, name):
+    """Bounds, scores, selection and both sparse decodes at one full-size
+    shape, keeping 50 % of every sequence's pages."""
     from latentserve_amd.kernels.hip import paged_sparse as ps
 
-    print("c5: sparse 50% B8 x 32768", flush=True)
-    q, k, v, t, l = config_case([32768] * 8, seed=5)
+    print(f"{name}: sparse 50% B{batch} x {ctx}", flush=True)
+    q, k, v, t, l = config_case([ctx] * batch, seed=seed)
     Q, K, V, T, L = dev(q, k, v, t, l)
     nb = k.shape[0]
     kmin = torch.empty(nb, H_KV, D, dtype=torch.float16, device="cuda")
@@ -192,29 +195,43 @@ def test_c5_sparse_half_b8x32k():
 
     width = t.shape[1]
     kk = oracle.budget(0.5, width)
-    assert kk == 1024
+    assert kk == ctx // PAGE // 2
     want_scores = oracle.page_scores(q, want_min, want_max, t, l)
     got_scores = ps.page_scores(Q, kmin, kmax, T, L).cpu().numpy()
     fin = np.isfinite(want_scores)                 # forced pages +inf, past the end -inf
     assert np.array_equal(got_scores[~fin], want_scores[~fin])
-    assert_close(got_scores[fin], want_scores[fin], 1e-3, 1e-4, "c5 scores")
+    assert_close(got_scores[fin], want_scores[fin], 1e-3, 1e-4, f"{name} scores")
 
     want_sel = oracle.select(want_scores, kk)
     got_sel = ps.index_select(Q, kmin, kmax, T, L, kk, 0.5).cpu().numpy()
-    _sets_agree(got_sel, want_sel, want_scores, "c5 selection")
+    _sets_agree(got_sel, want_sel, want_scores, f"{name} selection")
 
     want = oracle.sparse_decode(q, k, v, t, l, np.ascontiguousarray(got_sel), ratio=0.5)
     got_list = ps.sparse_decode(Q, K, V, T, L, torch.from_numpy(got_sel).cuda(), ratio=0.5)
     torch.cuda.synchronize()
-    assert_close(got_list.float().cpu().numpy(), want, ATOL, RTOL, "c5 list decode")
-    got_fused = ps.sparse_attention(Q, K, V, T, L, kmin, kmax, ratio=0.5, max_seq_len=32768)
+    assert_close(got_list.float().cpu().numpy(), want, ATOL, RTOL, f"{name} list decode")
+    # the benchmark's call: scoring, selection and attention in one launch
+    got_fused = ps.sparse_attention(Q, K, V, T, L, kmin, kmax, ratio=0.5, max_seq_len=ctx)
     torch.cuda.synchronize()
-    assert_close(got_fused.float().cpu().numpy(), want, ATOL, RTOL, "c5 selecting decode")
+    assert_close(got_fused.float().cpu().numpy(), want, ATOL, RTOL,
+                 f"{name} selecting decode")
     # and the oracle's own selection gives the same output where the sets agree
     if all(set(got_sel[i, j].tolist()) == set(want_sel[i, j].tolist())
-           for i in range(8) for j in range(H_KV)):
+           for i in range(batch) for j in range(H_KV)):
         want2 = oracle.sparse_decode(q, k, v, t, l, want_sel, ratio=0.5)
-        assert_close(got_fused.float().cpu().numpy(), want2, ATOL, RTOL, "c5 vs oracle select")
+        assert_close(got_fused.float().cpu().numpy(), want2, ATOL, RTOL,
+                     f"{name} vs oracle select")
+
+
+def test_c5_sparse_half_b8x32k():
+    _sparse_half_at_full_size(8, 32768, seed=5, name="c5")
+
+
+def test_c5h_sparse_half_b16x16k():
+    """The headline shape with half of every sequence's pages kept (the
+    reference reports its sparse pipeline at B16 x 16K:
+    docs/phase14_sparse.md:130)."""
+    _sparse_half_at_full_size(16, 16384, seed=51, name="c5h")
 
 
 def _fp32_decode_reference(model, ctx_len, ids, positions):
