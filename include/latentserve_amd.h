@@ -203,6 +203,11 @@ int ls_page_scores(const void* q, const int64_t* q_strides, const void* kmin, co
  * and attends as ls_sparse_attention_fp16 does.  A workgroup that does not
  * see every share stored within 50 us computes the scores it needs itself,
  * so no workgroup depends on another being resident.
+ * THE COUNT WORDS MUST START AT ALL ONES (0xFFFFFFFF): a word left anywhere
+ * in [0, num_splits - 2] (a zero-filled buffer, a launch that was aborted)
+ * lets the readers take a row before every share is stored, and the
+ * selection is then silently wrong; other values only cost the 50 us
+ * fallback.  Fill a new score buffer with 0xFF bytes before its first call.
  * Replaces the index + select + attend steps of sparse_attention
  * (kernels/cuda/paged_sparse.py:222-251; page_index, paged_sparse_fp16.cu:
  * 78-130).  k <= max_pages <= 2048 (COOP_MAX_PAGES), n_rep <= 8

@@ -427,6 +427,40 @@ def test_one_launch_bounds_path_matches_three_launches_and_the_oracle(h_kv, n_re
         assert (one.float() - three.float()).abs().max().item() < 1e-3, rep
 
 
+@pytest.mark.parametrize("order,width,splits", [("rising", 2048, 32), ("falling", 2048, 32),
+                                                 ("chunks", 2048, 16), ("rising", 300, 5),
+                                                 ("chunks", 1024, 16)])
+def test_one_launch_path_with_skewed_shares(order, width, splits):
+    """Page scores laid out so that the workgroups' shares of a row hold very
+    different numbers of selected pages (rising / falling with the page, or
+    alternating chunks of high and low pages): the one-launch path's
+    partition moves a share's surplus to the groups short of pages, and the
+    pages each group requested before the selection (its share's best) are
+    often not its items or not selected at all.  Every selected page must
+    still be attended exactly once: the output equals the three-launch path
+    and the oracle over the same lists."""
+    lens = [width * 16, width * 16 - 37]
+    q, k, v, t, l, kmin, kmax = index_case(lens, width=width, seed=width + 3)
+    q = np.abs(q)                            # scores monotone in the bounds below
+    pages = np.arange(width)
+    c = {"rising": pages / width, "falling": 1.0 - pages / width,
+         "chunks": ((pages // 96) % 2) + pages / (4.0 * width)}[order]
+    for b in range(len(lens)):
+        kmin[t[b]] = kmax[t[b]] = c.astype(np.float16)[:, None, None]
+    Q, K, V, T, L, KN, KX = dev(q, k, v, t, l, kmin, kmax)
+    ratio = 0.5
+    kk = ps().budget(ratio, width)
+    sel = ps().index_select(Q, KN, KX, T, L, kk, ratio).cpu().numpy()
+    want = oracle.sparse_decode(q, k, v, t, l, sel, ratio=ratio, recent=2)
+    for rep in range(2):
+        one = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=ratio, num_splits=splits)
+        three = ps().sparse_attention(Q, K, V, T, L, KN, KX, ratio=ratio, num_splits=splits,
+                                      fused=False)
+        torch.cuda.synchronize()
+        assert_close(one.float().cpu().numpy(), want, ATOL, RTOL, f"{order}, rep {rep}")
+        assert (one.float() - three.float()).abs().max().item() < 1e-3, (order, rep)
+
+
 @pytest.mark.parametrize("width,lens,splits", [(2048, [2048 * 16, 5000], 32), (300, [4800, 7], 5)])
 def test_one_launch_path_with_the_fallback_forced(width, lens, splits):
     """With the wait bound at 0 every workgroup of the one-launch path scores
