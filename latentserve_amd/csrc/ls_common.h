@@ -217,6 +217,21 @@ __device__ __forceinline__ int xcd_major(int L, int N) {
     return x * q + (x < rem ? x : rem) + L / XCDS;
 }
 
+// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding).
+constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Wait until at most n vector memory instructions of this wave are
+// outstanding, as a compiler barrier for memory: the compiler does not track
+// the LDS writes of direct-to-LDS loads, so LDS reads of their data follow
+// such a wait (n counted from the instructions issued after those loads).
+template <int N_AFTER>
+__device__ __forceinline__ void wait_vm_lds() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_wait(N_AFTER));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ __forceinline__ void handoff_release() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);

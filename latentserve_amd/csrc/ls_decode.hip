@@ -101,21 +101,37 @@ struct PageBuf {
     int res;      // INT8: this page's K comes from the residual
 };
 
+// An fp16 page's K rows (16 x 256 bytes of one head) are brought to a 4 KB
+// LDS slot of the wave by direct loads, each a whole 256-byte row to 16
+// lanes (four rows a load instruction), and read back in the MFMA layout
+// (row c per lane): loaded straight to registers in that layout, every load
+// instruction covers 64 bytes of each of 16 rows, half of each cache line,
+// and a read-only probe of the B16 x 16K pages ran 46.5 us that way against
+// 42.5 us through LDS.  Within a row the sixteen 16-byte pieces are stored
+// XOR-permuted by the row (piece p holds piece p ^ row), so the 16 lanes
+// that read one piece of 16 rows hit 16 different bank groups.
+constexpr int KSLOT_BYTES = PAGE * HEAD_DIM * 2;
+typedef __attribute__((address_space(3))) void* lds_ptr;
+// Vector memory instructions of one fp16 page request: 4 direct K loads, 4 V.
+constexpr int FP16_PAGE_VM = 8;
+
 template <int KIND, bool ASYM, bool HAS_RES>
 __device__ __forceinline__ void load_page(const DecodeParams& a, PageBuf& buf, int blk, int page,
                                           int num_pages, int res_row, int h, int g, int c,
-                                          bool fetch = true) {
+                                          bool fetch = true, char* kslot = nullptr) {
     // (blk and h are the same in every lane: the wave's item)
     const int64_t base = (int64_t)blk * a.sk_b + (int64_t)h * a.sk_h;
     if (KIND == KV_FP16) {
         const __amdgpu_buffer_rsrc_t rk = page_rsrc((const half_t*)a.k_pool + base, fetch);
         const __amdgpu_buffer_rsrc_t rv = page_rsrc((const half_t*)a.v_pool + base, fetch);
-        const int ko = (int)(((int64_t)c * a.sk_p + 8 * g) * sizeof(half_t));
         const int vo = (int)(((int64_t)(4 * g) * a.sk_p + 8 * c) * sizeof(half_t));
         const int row = (int)(a.sk_p * sizeof(half_t));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            buf.k[j] = page_load16(rk, ko + 64 * j);
+        for (int i = 0; i < 4; ++i) {
+            // lanes (g, c): row 4i + g, LDS piece c <- the row's piece c ^ row
+            const int r = 4 * i + g;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr)(kslot + 1024 * i), 16,
+                                                     r * row + ((c ^ r) << 4), 0, 0, PAGE_POLICY);
             issue_here();
         }
 #pragma unroll
@@ -740,13 +756,22 @@ __device__ float score_one(const DecodeParams& a, int b, int h, int len, int p) 
 // scoring its share of its sequence's pages (score_slice).
 template <int KIND, bool ASYM, bool HAS_RES, int SPARSE, int NWT, int HG, int ABL = 0>
 __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodeParams a) {
-    // Pages in flight ahead of the one being computed.  INT8 keeps one: a
-    // second buffer measured slower (c4 35.3 -> 39.1 us; with the page loads
-    // as inline asm and the walk's own waits, 37.5 us at one head a group,
+    // Pages in flight ahead of the one being computed: one.  INT8: a second
+    // buffer measured slower (c4 35.3 -> 39.1 us; with the page loads as
+    // inline asm and the walk's own waits, 37.5 us at one head a group,
     // spills at two), and a third takes the kernel to one wave a SIMD.
-    constexpr int PF_DEPTH = KIND == KV_FP16 ? 2 : 1;
+    // fp16 with K through LDS: the read-only probe of the B16 x 16K pages
+    // ran 42.5 us with one page in flight, 43.7 us with two.
+    constexpr int PF_DEPTH = 1;
     constexpr int NB = PF_DEPTH + 1;
     __shared__ DecodeSmem<NWT, HG, KIND == KV_INT8> sm;
+    // fp16: the waves' K slots, one array a buffer: the compiler holds an
+    // LDS access back until every direct load that may write its object is
+    // done, so the slots are objects apart from each other and from the
+    // item claims and the table
+    __shared__ __attribute__((aligned(16))) char kstage0[KIND == KV_FP16 ? NWT * KSLOT_BYTES : 16];
+    __shared__ __attribute__((aligned(16))) char kstage1[KIND == KV_FP16 ? NWT * KSLOT_BYTES : 16];
+
     LS_STAMP(0);
 #ifdef LS_STAMPS
     if (threadIdx.x == 0)           // stamp 15: the XCD this group runs on
@@ -839,9 +864,11 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     };
     load_q(hb);
 
-    // Page buffers in rotation: items k+1 and k+2 are in flight while item k
-    // is computed, and the item after is being claimed.
+    // Page buffers in rotation: item k+1 is in flight while item k is
+    // computed, and the item after is being claimed.
     PageBuf buf[NB];
+    auto kslot = [&](int slot) { return (slot == 0 ? kstage0 : kstage1) + wv * KSLOT_BYTES; };
+    static_assert(NB == 2, "one K slot array a page buffer");
     int item[NB], pgs[NB], blks[NB];
     auto issue_raw = [&](int slot, int it, int blk, int pg) {
         item[slot] = it;
@@ -857,7 +884,19 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         const int safe_blk = valid ? blk : 0;
         const bool fetch = valid;
         load_page<KIND, ASYM, KIND == KV_FP16 && HAS_RES>(a, buf[slot], safe_blk, -1, 0, 0,
-                                                          h0 + hw, g, c, fetch);
+                                                          h0 + hw, g, c, fetch, kslot(slot));
+    };
+    // fp16: the K rows of the page in buffer `slot`, from its LDS slot into
+    // the MFMA layout (row c; pieces 4j + g, stored at (4j + g) ^ c)
+    auto k_from_lds = [&](int slot) {
+        if constexpr (KIND == KV_FP16) {
+            // that page's direct loads are done once no more than its own V
+            // loads and the PF_DEPTH later pages' requests are outstanding
+            wait_vm_lds<4 + FP16_PAGE_VM * PF_DEPTH>();
+            const char* rowp = kslot(slot) + c * 256;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) buf[slot].k[j] = *(const u4*)(rowp + (((4 * j + g) ^ c) << 4));
+        }
     };
     // Which sequence and split this group serves: the host grid's for a
     // page-subset walk, else the length-proportional deal.
@@ -1162,6 +1201,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 // force conservative waits on the next reuse of its registers
                 const bool ok_u = live(u);
                 const int live_len = ok_u ? len : 0;
+                k_from_lds(u);
                 if (ABL == 1 || ABL == 2)
                     consume_page<KIND>(buf[u], st);
                 else
@@ -1186,6 +1226,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         walk(resolve_lds, first_mem);
     else
         walk(resolve_mem, first_mem);
+    // (fp16: the direct K loads of items past the end may still be writing
+    // the wave's slots; none may land after the group ends)
+    if constexpr (KIND == KV_FP16) wait_vm_lds<0>();
     LS_STAMP(8);
 
     const int NR = a.NR;

@@ -111,8 +111,6 @@ __device__ __forceinline__ int w_row(const GemmParams& a, int tile, int r) {
 // ((T * steps + s) * 64 + lane) * 8 halves.
 constexpr int GEMM_PACK_TILES = 4;    // tiles padded to a multiple of the largest TPW
 
-// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding).
-constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // LDS rows of a wave's X chunk (one column block, 16 steps): 16 rows of 512
 // channels, padded by 16 bytes so the rows of a 16-lane read fall in

@@ -114,7 +114,22 @@ __device__ __attribute__((always_inline)) void select_keys(const float* srow, in
     if constexpr (COOP) {
         const bool done = fix.wait();   // the row's writers say they are done
         LS_STAMP(3);
-        if (done) {
+        if (done && ((uintptr_t)srow & 15) == 0) {
+            // a 16-byte aligned row: 16-byte device-coherent loads over a
+            // resource of the row's P words (lanes past it read zeros);
+            // against one 4-byte load a key, B8 x 32K 45.63 -> 45.10 us
+            static_assert(KPT % 4 == 0, "keys in 16-byte pieces");
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc((void*)srow, 0, P * 4, 0x00020000);
+#pragma unroll
+            for (int j = 0; j < KPT; j += 4) {
+                const f4 v = load_coherent4(rs, (i0 + j) * 4);
+                f[j] = v[0];
+                f[j + 1] = v[1];
+                f[j + 2] = v[2];
+                f[j + 3] = v[3];
+            }
+        } else if (done) {
 #pragma unroll
             for (int j = 0; j < KPT; ++j)
                 f[j] = P > 0 ? load_coherent(srow + (i0 + j < last ? i0 + j : last)) : 0.f;

@@ -308,8 +308,9 @@ def sparse_attention(q, k_pool, v_pool, block_tables, seq_lens, kmin, kmax,
         # ones at rest
         _check_bounds(kmin, kmax, q.device)
         # (each row is followed by one word: the count of its scored shares)
-        ws = scratch("sparse_coop_scores", (b, h, block_tables.shape[1] + 1), torch.int32,
-                     q.device, init=-1)
+        # (rows padded to 16 bytes, so a row starts 16-byte aligned)
+        ws = scratch("sparse_coop_scores", (b, h, (block_tables.shape[1] + 4) // 4 * 4),
+                     torch.int32, q.device, init=-1)
         rc = _lib.lib().ls_sparse_attention_bounds_fp16(
             P(q), S(q, 3), P(k_pool), P(v_pool), S(k_pool, 3), k_pool.shape[0],
             P(block_tables), block_tables.stride(0), block_tables.shape[1], P(seq_lens),

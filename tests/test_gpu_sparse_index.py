@@ -486,7 +486,7 @@ def test_one_launch_path_with_the_fallback_forced(width, lens, splits):
     assert_close(forced.float().cpu().numpy(), want, ATOL, RTOL, "fallback forced")
     from latentserve_amd.kernels.gqa import _SCRATCH
     for key, buf in _SCRATCH.items():
-        if key[0] == "sparse_coop_scores":
+        if key[0] == "sparse_coop_scores" and buf.shape[2] == (width + 4) // 4 * 4:
             # the word after every row (the count after each head group's
             # first row; untouched after the others)
-            assert bool((buf[:, :, -1] == -1).all()), "count words not left all ones"
+            assert bool((buf[:, :, width] == -1).all()), "count words not left all ones"
