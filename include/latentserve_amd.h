@@ -64,6 +64,30 @@ const char* ls_last_error(void);
 /* ABI version (bumped on any signature change or addition). */
 int ls_abi_version(void);
 
+/* What the runtime reports of a loaded kernel (hipFuncGetAttributes and
+ * hipOccupancyMaxActiveBlocksPerMultiprocessor).  Replaces the reference's
+ * kernel_resources (kernels/cuda/paged_decode_cuda.py:163-186, CUDA driver
+ * function attributes; kernels/cuda/paged_sparse.py:254-265). */
+typedef struct LsKernelResources {
+    int regs;           /* vector registers a lane */
+    int local_bytes;    /* private (spill) memory a lane: 0 means no spills */
+    int shared_bytes;   /* static LDS a workgroup */
+    int threads;        /* threads a workgroup of its launches */
+    int groups_per_cu;  /* workgroups one CU holds at once */
+} LsKernelResources;
+
+/* `kernel`: "paged_decode_fp16", "paged_decode_int8" (asym, has_res: zero
+ * points, fp16 last-page K), "paged_sparse_fp16" (a given list),
+ * "sparse_attention_fp16" (selecting from given scores),
+ * "sparse_attention_bounds_fp16" (one launch), "combine_splits",
+ * "page_index", "page_index_heads", "page_mass", "page_select",
+ * "page_bounds_update", "page_bounds_rebuild", "int8_decode_write",
+ * "int8_finalize_blocks".  kv_heads: decode kernels pair the heads of an
+ * even count in one workgroup; n_rep: the index kernels are specialised on
+ * it.  Needs a current HIP device. */
+int ls_kernel_resources(const char* kernel, int kv_heads, int n_rep, int asym, int has_res,
+                        LsKernelResources* out);
+
 /* Bytes of `workspace` a decode call with these sizes needs (0 when
  * num_splits == 1).  No counterpart in the reference, which sizes its
  * partial buffers in Python (kernels/gqa/paged_decode.py:783-787). */

@@ -28,11 +28,12 @@ LS_ERR_INVALID = 1
 LS_ERR_HIP = 2
 # The ABI this binding is written for (include/latentserve_amd.h); a library
 # built from other sources is refused rather than called with wrong arguments.
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 # name -> argtypes, mirroring include/latentserve_amd.h
 _SIGNATURES = {
     "ls_abi_version": [],
+    "ls_kernel_resources": [ctypes.c_char_p, _I32, _I32, _I32, _I32, _VP],
     "ls_last_error": [],
     "ls_decode_workspace_bytes": [_I32, _I32, _I32, _I32],
     "ls_decode_counter_ints": [_I32, _I32],
@@ -167,6 +168,26 @@ def strides(t: Optional[torch.Tensor], n: int):
     if t is None:
         return None
     return (ctypes.c_int64 * n)(*t.stride()[:n])
+
+
+class KernelResources(ctypes.Structure):
+    """LsKernelResources (include/latentserve_amd.h)."""
+    _fields_ = [("regs", ctypes.c_int), ("local_bytes", ctypes.c_int),
+                ("shared_bytes", ctypes.c_int), ("threads", ctypes.c_int),
+                ("groups_per_cu", ctypes.c_int)]
+
+
+def kernel_resources(kernel: str, device: Optional[torch.device] = None, kv_heads: int = 2,
+                     n_rep: int = 6, asym: bool = False, has_res: bool = False) -> dict:
+    """ls_kernel_resources for one kernel, as a dict, on `device` (default:
+    the current one)."""
+    r = KernelResources()
+    dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    with torch.cuda.device(dev):
+        rc = lib().ls_kernel_resources(kernel.encode(), int(kv_heads), int(n_rep), int(asym),
+                                       int(has_res), ctypes.byref(r))
+    check(rc, "ls_kernel_resources")
+    return {name: int(getattr(r, name)) for name, _ in KernelResources._fields_}
 
 
 def stream_of(device: torch.device):

@@ -230,7 +230,40 @@ extern "C" {
 
 const char* ls_last_error(void) { return g_err.c_str(); }
 
-int ls_abi_version(void) { return 18; }
+int ls_abi_version(void) { return 19; }
+
+int ls_kernel_resources(const char* kernel, int kv_heads, int n_rep, int asym, int has_res,
+                        LsKernelResources* out) {
+    if (!kernel || !out) return fail(LS_ERR_INVALID, "null pointer argument");
+    if (kv_heads < 1 || n_rep < 1 || n_rep > ls::MAX_NREP)
+        return fail(LS_ERR_INVALID, "bad kv_heads (%d) or n_rep (%d)", kv_heads, n_rep);
+    const std::string k = kernel;
+    const bool pair = kv_heads % 2 == 0;
+    ls::KernelResources r{};
+    hipError_t e;
+    if (k == "paged_decode_fp16") e = ls::decode_resources(ls::KV_FP16, 0, false, false, pair, &r);
+    else if (k == "paged_decode_int8") e = ls::decode_resources(ls::KV_INT8, 0, asym, has_res, pair, &r);
+    else if (k == "paged_sparse_fp16") e = ls::decode_resources(ls::KV_FP16, 1, false, false, pair, &r);
+    else if (k == "sparse_attention_fp16") e = ls::decode_resources(ls::KV_FP16, 2, false, false, pair, &r);
+    else if (k == "sparse_attention_bounds_fp16") e = ls::decode_resources(ls::KV_FP16, 3, false, false, pair, &r);
+    else if (k == "combine_splits") e = ls::combine_resources(&r);
+    else if (k == "page_index") e = ls::sparse_index_resources(0, n_rep, &r);
+    else if (k == "page_index_heads") e = ls::sparse_index_resources(1, n_rep, &r);
+    else if (k == "page_mass") e = ls::sparse_index_resources(2, n_rep, &r);
+    else if (k == "page_select") e = ls::sparse_index_resources(3, n_rep, &r);
+    else if (k == "page_bounds_update") e = ls::sparse_index_resources(4, n_rep, &r);
+    else if (k == "page_bounds_rebuild") e = ls::sparse_index_resources(5, n_rep, &r);
+    else if (k == "int8_decode_write") e = ls::int8_write_resources(0, &r);
+    else if (k == "int8_finalize_blocks") e = ls::int8_write_resources(1, &r);
+    else return fail(LS_ERR_INVALID, "unknown kernel '%s'", kernel);
+    if (e != hipSuccess) return hip_status(e, "ls_kernel_resources");
+    out->regs = r.regs;
+    out->local_bytes = r.local_bytes;
+    out->shared_bytes = r.shared_bytes;
+    out->threads = r.threads;
+    out->groups_per_cu = r.groups_per_cu;
+    return LS_OK;
+}
 
 // The bound on the one-launch bounds path's wait for the other workgroups'
 // scores (ls_set_coop_wait_ticks).

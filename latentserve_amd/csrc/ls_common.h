@@ -232,6 +232,23 @@ __device__ __forceinline__ void wait_vm_lds() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// What the runtime reports of a loaded kernel (ls_kernel_resources).
+struct KernelResources {
+    int regs, local_bytes, shared_bytes, threads, groups_per_cu;
+};
+template <class F>
+inline hipError_t func_resources(F* fn, int threads, KernelResources* r) {
+    hipFuncAttributes at;
+    hipError_t e = hipFuncGetAttributes(&at, reinterpret_cast<const void*>(fn));
+    if (e != hipSuccess) return e;
+    r->regs = at.numRegs;
+    r->local_bytes = (int)at.localSizeBytes;
+    r->shared_bytes = (int)at.sharedSizeBytes;
+    r->threads = threads;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&r->groups_per_cu,
+                                                        reinterpret_cast<const void*>(fn), threads, 0);
+}
+
 __device__ __forceinline__ void handoff_release() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);

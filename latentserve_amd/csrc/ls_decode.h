@@ -6,6 +6,8 @@
 
 namespace ls {
 
+struct KernelResources;   // ls_common.h
+
 enum KvKind { KV_FP16 = 0, KV_INT8 = 1 };
 
 // List entries one group of a selecting page-subset walk keeps in its item
@@ -98,6 +100,12 @@ constexpr int NOALLOC_COUNTERS = 1 << 16;
 // at the first call on the device).
 hipError_t noalloc_scratch(hipStream_t stream, float** work, int32_t** counters);
 hipError_t launch_combine(const CombineParams& p, hipStream_t stream);
+// The kernel a decode launch runs: walk 0 dense, 1 a given list, 2 selecting
+// from given scores, 3 scoring and selecting itself; `pair_heads` an even
+// head count; INT8 with `asym` / `has_res`.  combine: ls_combine_splits's.
+hipError_t decode_resources(int kind, int walk, bool asym, bool has_res, bool pair_heads,
+                            KernelResources* r);
+hipError_t combine_resources(KernelResources* r);
 #ifdef LS_DIAGNOSTICS
 // Page-compute probe (measurement only): groups x 8 waves, each applying one
 // register-resident page `items` times; mode 0 MFMA (compute_page), 1 VALU.

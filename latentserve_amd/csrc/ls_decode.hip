@@ -978,14 +978,20 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     constexpr int ENT_INTS = DecodeSmem<NWT, HG, KIND == KV_INT8>::ENT_INTS;
     constexpr int CAP = SPARSE ? ENT_INTS / (2 * HG) : ENT_INTS;
     const bool cached = n_ent <= CAP;
-    auto resolve_global = [&](int e, int hh, int& blk, int& pg) {
-        pg = SPARSE ? a.sel[(int64_t)b * a.ssel_b + (int64_t)(h0 + hh) * a.ssel_h + lo + e] : lo + e;
-        blk = -1;
+    // (an item's block and page, returned by value: resolvers writing
+    // through references put the pair in a stack slot of the general walk)
+    struct ItemRef {
+        int blk, pg;
+    };
+    auto resolve_global = [&](int e, int hh) -> ItemRef {
+        const int pg =
+            SPARSE ? a.sel[(int64_t)b * a.ssel_b + (int64_t)(h0 + hh) * a.ssel_h + lo + e] : lo + e;
+        int blk = -1;
         if (pg >= 0 && pg < num_pages) {
-            blk = a.block_tables[(int64_t)b * a.sbt_b + pg];
-            if (blk < 0 || blk >= a.num_blocks) blk = -1;
-            if (HAS_RES && pg == num_pages - 1 && !res_ok) blk = -1;
+            const int t = a.block_tables[(int64_t)b * a.sbt_b + pg];
+            blk = t < 0 || t >= a.num_blocks || (HAS_RES && pg == num_pages - 1 && !res_ok) ? -1 : t;
         }
+        return {blk, pg};
     };
     auto fill_table = [&]() {
         if (!cached) return;
@@ -1082,10 +1088,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         } else if (SPARSE) {
             for (int i = threadIdx.x; i < n_ent * HG; i += WAVE * NWT) {
                 const int hh = i / n_ent, e = i % n_ent;
-                int blk, pg;
-                resolve_global(e, hh, blk, pg);
-                sm.ent[(hh * 2) * CAP + e] = blk;
-                sm.ent[(hh * 2 + 1) * CAP + e] = pg;
+                const ItemRef r = resolve_global(e, hh);
+                sm.ent[(hh * 2) * CAP + e] = r.blk;
+                sm.ent[(hh * 2 + 1) * CAP + e] = r.pg;
             }
         } else {
             for (int e = threadIdx.x; e < n_ent; e += WAVE * NWT) {
@@ -1093,8 +1098,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
                 int blk = e == (int)threadIdx.x && spec_ok ? spec_blk : -2;
                 const int pg = lo + e;
                 if (blk == -2 || !(pg >= 0 && pg < num_pages)) {
-                    int p2;
-                    resolve_global(e, 0, blk, p2);
+                    blk = resolve_global(e, 0).blk;
                 } else {
                     if (blk < 0 || blk >= a.num_blocks) blk = -1;
                     if (HAS_RES && pg == num_pages - 1 && !res_ok) blk = -1;
@@ -1117,32 +1121,20 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // unresolvable come back with blk -1: their buffer is filled from block 0
     // (any valid address: it keeps every iteration's loads and waits
     // identical) and computed with every token masked.
-    auto resolve_lds = [&](int i, int& blk, int& pg) {
-        if (i >= n_items) {
-            blk = -1;
-            pg = -1;
-        } else if (SPARSE) {
-            blk = sm.ent[(hw * 2) * CAP + i];
-            pg = sm.ent[(hw * 2 + 1) * CAP + i];
-        } else {
-            blk = sm.ent[i];
-            pg = lo + i;
-        }
+    auto resolve_lds = [&](int i) -> ItemRef {
+        if (i >= n_items) return {-1, -1};
+        if (SPARSE) return {sm.ent[(hw * 2) * CAP + i], sm.ent[(hw * 2 + 1) * CAP + i]};
+        return {sm.ent[i], lo + i};
     };
     // The wave's fixed item u (dense walk with the host's split): its block
     // is in lane u of first_blk.  Returned unchecked: the sequence length is
     // not needed to request the page (issue_with checks the item afterwards).
-    auto resolve_first = [&](int u, int i, int& blk, int& pg) {
-        pg = spec_lo + i;
-        blk = __builtin_amdgcn_readlane(first_blk, u);
+    auto resolve_first = [&](int u, int i) -> ItemRef {
+        return {__builtin_amdgcn_readlane(first_blk, u), spec_lo + i};
     };
-    auto resolve_mem = [&](int i, int& blk, int& pg) {
-        if (i >= n_items) {
-            blk = -1;
-            pg = -1;
-        } else {
-            resolve_global(i, hw, blk, pg);
-        }
+    auto resolve_mem = [&](int i) -> ItemRef {
+        if (i >= n_items) return {-1, -1};
+        return resolve_global(i, hw);
     };
 
     auto live = [&](int slot) {
@@ -1166,9 +1158,8 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
             }
         }
         auto issue_with = [&](auto res, int slot, int it) {
-            int blk, pg;
-            res(it, blk, pg);
-            issue_raw(slot, it, blk, pg);
+            const ItemRef r = res(it);
+            issue_raw(slot, it, r.blk, r.pg);
         };
         auto issue = [&](int slot, int it) { issue_with(resolve, slot, it); };
         // The first items are fixed (wave wl of a head takes wl, wl + NWH, ...): their
@@ -1181,7 +1172,7 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         }
 #pragma unroll
         for (int u = 0; u < PF_DEPTH; ++u)
-            issue_with([&](int i, int& blk, int& pg) { first(u, i, blk, pg); }, u, wl + u * NWH);
+            issue_with([&](int i) { return first(u, i); }, u, wl + u * NWH);
         if (SPARSE < 2) {
             fill_table();
             __syncthreads();
@@ -1215,9 +1206,9 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // Separate instantiations for the fast path (the host's split covers the
     // sequence and the item table fits in LDS) and the general ones, so no
     // fallback load shares the fast path's control flow.
-    auto first_fixed = [&](int u, int i, int& blk, int& pg) { resolve_first(u, i, blk, pg); };
-    auto first_mem = [&](int, int i, int& blk, int& pg) { resolve_mem(i, blk, pg); };
-    auto first_lds = [&](int, int i, int& blk, int& pg) { resolve_lds(i, blk, pg); };
+    auto first_fixed = [&](int u, int i) { return resolve_first(u, i); };
+    auto first_mem = [&](int, int i) { return resolve_mem(i); };
+    auto first_lds = [&](int, int i) { return resolve_lds(i); };
     if (SPARSE >= 2)
         walk(resolve_lds, first_lds);      // the host keeps every range within the table
     else if (cached && spec_ok)
@@ -1463,6 +1454,35 @@ static hipError_t launch_kernel(const DecodeParams& a, hipStream_t stream) {
     return launch_t<KV_INT8, false, false, 0>(a, stream);
 }
 
+template <int KIND, bool ASYM, bool HAS_RES, int SPARSE>
+static hipError_t resources_t(bool pair_heads, KernelResources* r) {
+    if (pair_heads)
+        return func_resources(paged_decode_kernel<KIND, ASYM, HAS_RES, SPARSE, 2 * NWAVES, 2>,
+                              WAVE * NWAVES * 2, r);
+    return func_resources(paged_decode_kernel<KIND, ASYM, HAS_RES, SPARSE, NWAVES, 1>,
+                          WAVE * NWAVES, r);
+}
+
+hipError_t decode_resources(int kind, int walk, bool asym, bool has_res, bool pair_heads,
+                            KernelResources* r) {
+    if (kind == KV_FP16) {
+        switch (walk) {
+            case 0: return resources_t<KV_FP16, false, false, 0>(pair_heads, r);
+            case 1: return resources_t<KV_FP16, false, false, 1>(pair_heads, r);
+            case 2: return resources_t<KV_FP16, false, false, 2>(pair_heads, r);
+            case 3: return resources_t<KV_FP16, false, false, 3>(pair_heads, r);
+            default: return hipErrorInvalidValue;
+        }
+    }
+    if (walk != 0) return hipErrorInvalidValue;
+    if (asym && has_res) return resources_t<KV_INT8, true, true, 0>(pair_heads, r);
+    if (asym) return resources_t<KV_INT8, true, false, 0>(pair_heads, r);
+    if (has_res) return resources_t<KV_INT8, false, true, 0>(pair_heads, r);
+    return resources_t<KV_INT8, false, false, 0>(pair_heads, r);
+}
+
+hipError_t combine_resources(KernelResources* r) { return func_resources(combine_kernel<4>, 256, r); }
+
 hipError_t launch_decode(const DecodeParams& a, hipStream_t stream) {
     return launch_kernel(a, stream);
 }
@@ -1701,12 +1721,22 @@ hipError_t noalloc_scratch(hipStream_t stream, float** work, int32_t** counters)
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return e;
         if (!p) return hipErrorInvalidSymbol;
-        int32_t* cnt = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(p) +
-                                                  NOALLOC_WORK_BYTES);
-        hipLaunchKernelGGL(zero_i32_kernel, dim3((NOALLOC_COUNTERS + 255) / 256), dim3(256), 0,
-                           stream, cnt, NOALLOC_COUNTERS);
-        e = hipGetLastError();
+        // The array is zero when the code object is loaded (a static
+        // __device__ array with no initializer), so the counters start at
+        // zero; they are cleared once more here unless the first call is
+        // being captured into a graph, where the clear would only be
+        // recorded (and re-run by every replay), not run now.
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cap);
         if (e != hipSuccess) return e;
+        if (cap == hipStreamCaptureStatusNone) {
+            int32_t* cnt = reinterpret_cast<int32_t*>(static_cast<unsigned char*>(p) +
+                                                      NOALLOC_WORK_BYTES);
+            hipLaunchKernelGGL(zero_i32_kernel, dim3((NOALLOC_COUNTERS + 255) / 256), dim3(256), 0,
+                               stream, cnt, NOALLOC_COUNTERS);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
         g_scratch_ptr[dev] = p;
     }
     unsigned char* base = static_cast<unsigned char*>(g_scratch_ptr[dev]);

@@ -6,6 +6,8 @@
 
 namespace ls {
 
+struct KernelResources;   // ls_common.h
+
 struct QuantArgs {
     int asym;          // 0: symmetric absmax, 1: asymmetric min/max
     int recip;         // 1: x / qmax as x * fp32(1 / qmax) (torch on a GPU); 0: true division
@@ -44,5 +46,7 @@ struct FinalizeParams {
 
 hipError_t launch_decode_write(const DecodeWriteParams& p, hipStream_t stream);
 hipError_t launch_finalize_k(const FinalizeParams& p, hipStream_t stream);
+// what: 0 decode_write, 1 finalize_k
+hipError_t int8_write_resources(int what, KernelResources* r);
 
 }  // namespace ls

@@ -166,4 +166,10 @@ hipError_t launch_finalize_k(const FinalizeParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+hipError_t int8_write_resources(int what, KernelResources* r) {
+    if (what == 0) return func_resources(decode_write_kernel, 256, r);
+    if (what == 1) return func_resources(finalize_k_kernel, 256, r);
+    return hipErrorInvalidValue;
+}
+
 }  // namespace ls

@@ -7,6 +7,8 @@
 
 namespace ls {
 
+struct KernelResources;   // ls_common.h
+
 // Largest page count the selection keeps in registers (32 keys per thread of
 // a 256-thread group).
 constexpr int SELECT_MAX_PAGES = 8192;
@@ -63,5 +65,8 @@ hipError_t launch_page_select(const SelectParams& p, hipStream_t stream);
 hipError_t launch_page_mass(const IndexParams& p, hipStream_t stream);
 hipError_t launch_bounds_update(const BoundsParams& p, hipStream_t stream);
 hipError_t launch_bounds_rebuild(const BoundsParams& p, hipStream_t stream);
+// what: 0 page_index, 1 page_index_heads (mass), 2 page_mass, 3 page_select,
+// 4 bounds_update, 5 bounds_rebuild; index kernels at n_rep rows.
+hipError_t sparse_index_resources(int what, int n_rep, KernelResources* r);
 
 }  // namespace ls

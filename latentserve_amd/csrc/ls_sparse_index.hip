@@ -353,4 +353,26 @@ hipError_t launch_bounds_rebuild(const BoundsParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+hipError_t sparse_index_resources(int what, int n_rep, KernelResources* r) {
+    switch (what) {
+        case 3: return func_resources(page_select_kernel<false>, 256, r);
+        case 4: return func_resources(bounds_update_kernel, 64, r);
+        case 5: return func_resources(bounds_rebuild_kernel, 256, r);
+        default: break;
+    }
+    switch (n_rep) {
+#define LS_RES_NR(n)                                                               \
+    case n:                                                                        \
+        return what == 0   ? func_resources(page_index_kernel<n>, 256, r)          \
+               : what == 1 ? func_resources(page_index_kernel<n, true>, 256, r)    \
+               : what == 2 ? func_resources(page_mass_kernel<n>, 256, r)           \
+                           : hipErrorInvalidValue;
+        LS_RES_NR(1) LS_RES_NR(2) LS_RES_NR(3) LS_RES_NR(4) LS_RES_NR(5) LS_RES_NR(6)
+        LS_RES_NR(7) LS_RES_NR(8) LS_RES_NR(9) LS_RES_NR(10) LS_RES_NR(11)
+        LS_RES_NR(12) LS_RES_NR(13) LS_RES_NR(14) LS_RES_NR(15) LS_RES_NR(16)
+#undef LS_RES_NR
+        default: return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace ls

@@ -201,6 +201,51 @@ def paged_decode_hip(q, k_pool, v_pool, block_tables, seq_lens, max_seq_len: int
     return buf[:, :, :n_rep] if out is None else out
 
 
+def paged_decode_cuda(q, k_pool, v_pool, block_tables, seq_lens, max_seq_len: int,
+                      num_splits: Optional[int] = None,
+                      softmax_scale: Optional[float] = None,
+                      k_scale=None, v_scale=None, k_zero=None, v_zero=None,
+                      k_residual=None, res_rows=None,
+                      min_blocks: Optional[int] = None) -> torch.Tensor:
+    """The reference's launcher name and signature
+    (kernels/cuda/paged_decode_cuda.py:202-207), on the HIP kernels.
+
+    ``min_blocks`` is accepted and has no effect: the reference passes it to
+    NVRTC as the INT8 kernel's minimum resident blocks (a register cap);
+    these kernels are built ahead of time with fixed launch bounds (one
+    workgroup of 8 waves a CU), reported by ``kernel_resources``.
+    """
+    del min_blocks
+    return paged_decode_hip(q, k_pool, v_pool, block_tables, seq_lens, max_seq_len,
+                            num_splits=num_splits, softmax_scale=softmax_scale,
+                            k_scale=k_scale, v_scale=v_scale, k_zero=k_zero, v_zero=v_zero,
+                            k_residual=k_residual, res_rows=res_rows)
+
+
+def kernel_resources(device: Optional[torch.device] = None, head_dim: int = HEAD_DIM,
+                     n_rep: int = 6, page: int = PAGE, variant: str = "fp16",
+                     asym: bool = False, has_res: bool = False,
+                     min_blocks: Optional[int] = None, kv_heads: int = 2) -> dict:
+    """Registers, private (spill) memory and LDS of the loaded decode kernel
+    that a launch with these properties runs, as the HIP runtime reports
+    them (kernels/cuda/paged_decode_cuda.py:163-186, which asks the CUDA
+    driver): ``regs`` (vector registers a lane), ``local_bytes`` (0: no
+    spills), ``shared_bytes``, plus ``threads`` (a workgroup) and
+    ``groups_per_cu`` (occupancy).  ``min_blocks`` has no effect here (see
+    paged_decode_cuda); ``kv_heads`` chooses the paired-head kernel (even)
+    or the one-head kernel (odd).
+    """
+    del min_blocks
+    if head_dim != HEAD_DIM or page != PAGE or not 1 <= n_rep <= MAX_NREP:
+        raise ValueError(f"the HIP kernels are built for head_dim {HEAD_DIM}, page {PAGE} and "
+                         f"n_rep 1..{MAX_NREP}")
+    names = {"fp16": "paged_decode_fp16", "int8": "paged_decode_int8"}
+    if variant not in names:
+        raise ValueError(f"variant must be 'fp16' or 'int8', got {variant!r}")
+    return _lib.kernel_resources(names[variant], device, kv_heads=kv_heads, n_rep=n_rep,
+                                 asym=asym, has_res=has_res)
+
+
 def combine_splits_hip(partial_acc: torch.Tensor, partial_m: torch.Tensor,
                        partial_l: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     """combine_splits (kernels/gqa/paged_decode.py:689-706) as one HIP launch.

@@ -52,6 +52,17 @@ def _score_buffer(b: int, h: int, max_pages: int, device) -> torch.Tensor:
     return buf[:, :, :max_pages]
 
 
+def kernel_resources(device: Optional[torch.device] = None, n_rep: int = 6,
+                     kv_heads: int = 2) -> dict:
+    """Registers, private (spill) memory and LDS of each loaded page-subset
+    kernel, by name (kernels/cuda/paged_sparse.py:254-265; the reference's
+    four names plus this build's selection and one-launch kernels)."""
+    names = ("page_bounds_update", "page_index", "page_index_heads", "paged_sparse_fp16",
+             "page_mass", "page_select", "page_bounds_rebuild", "sparse_attention_fp16",
+             "sparse_attention_bounds_fp16")
+    return {n: _lib.kernel_resources(n, device, kv_heads=kv_heads, n_rep=n_rep) for n in names}
+
+
 def rebuild_bounds(k_pool: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor) -> None:
     """Every block's per-channel K bounds from the pool, over all PAGE rows."""
     _check_bounds(kmin, kmax, k_pool.device)

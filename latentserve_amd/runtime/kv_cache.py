@@ -58,15 +58,26 @@ class BlockAllocator:
         self._refs: List[int] = [0] * self.num_blocks
         self._stack: List[int] = []
         self.peak_used = 0
+        self.alloc_calls = 0
+        self.free_calls = 0
         self.reclaimer: Optional[Callable[[int], object]] = None
         self.reclaimable: Optional[Callable[[], int]] = None
         self.on_ref_change: Optional[Callable[[int, int, int], None]] = None
         self.reset()
 
     def reset(self) -> None:
-        """Every block free again, the pool as new."""
+        """Every block free again and the counters at zero: the pool as new."""
         self._refs = [0] * self.num_blocks
         self._stack = list(range(self.num_blocks - 1, -1, -1))   # top = lowest id
+        self.peak_used = self.alloc_calls = self.free_calls = 0
+
+    def stats(self) -> dict:
+        """The pool's occupancy and traffic, under the reference's keys
+        (cache/block_allocator.py:152-161)."""
+        return {"num_blocks": self.num_blocks, "block_size": self.block_size,
+                "blocks_used": self.num_used, "blocks_free": self.num_free,
+                "block_utilization": self.utilization, "peak_blocks_used": self.peak_used,
+                "alloc_calls": self.alloc_calls, "free_calls": self.free_calls}
 
     @property
     def num_free(self) -> int:
@@ -98,6 +109,7 @@ class BlockAllocator:
                               f"{self.num_blocks} are free")
         taken = self._stack[len(self._stack) - count:][::-1]
         del self._stack[len(self._stack) - count:]
+        self.alloc_calls += 1
         for b in taken:
             self._refs[b] = 1
         self.peak_used = max(self.peak_used, self.num_used)
@@ -114,6 +126,7 @@ class BlockAllocator:
     def free(self, blocks: Iterable[int]) -> None:
         """Drop one reference to each block; a block whose count reaches
         zero goes back on the stack."""
+        self.free_calls += 1
         for b in blocks:
             if not 0 <= b < self.num_blocks or self._refs[b] == 0:
                 raise ValueError(f"block {b} is already free")
@@ -146,12 +159,28 @@ class BlockTable:
         # mirror that saw an older lineage re-uploads the whole row
         self.lineage = 0
 
-    def append(self, num_tokens: int) -> None:
-        """Make room for num_tokens more tokens (new pages as needed)."""
+    @property
+    def capacity(self) -> int:
+        """Token slots of the table's pages."""
+        return len(self.blocks) * self.allocator.block_size
+
+    @property
+    def wasted_slots(self) -> int:
+        """Slots of the last page past the tokens written (internal
+        fragmentation, under one page a sequence)."""
+        return self.capacity - self.length
+
+    def reserve(self, num_tokens: int) -> None:
+        """Pages for length + num_tokens tokens, allocated as needed; the
+        length is unchanged (cache/block_allocator.py:198-208)."""
         need = self.allocator.blocks_for_tokens(self.length + num_tokens) - len(self.blocks)
         if need > 0:
             self.blocks.extend(self.allocator.allocate(need))
             self.version += 1
+
+    def append(self, num_tokens: int) -> None:
+        """Make room for num_tokens more tokens (new pages as needed)."""
+        self.reserve(num_tokens)
         self.length += num_tokens
 
     def slot(self, position: int) -> int:

@@ -39,7 +39,7 @@ def test_python_binding_covers_the_header():
 
 
 def test_abi_version(lib):
-    assert lib.ls_abi_version() == 18
+    assert lib.ls_abi_version() == 19
 
 
 def test_workspace_size(lib):
@@ -98,3 +98,15 @@ def test_noalloc_refuses_more_pairs_than_its_counters(lib):
                                           0.088, None)
     assert rc == 1
     assert "arrival counters" in lib.ls_last_error().decode()
+
+
+def test_kernel_resources_rejects_unknown_names_and_bad_shapes(lib):
+    """Argument checks of ls_kernel_resources, before any device call."""
+    from latentserve_amd import _lib
+    r = _lib.KernelResources()
+    assert lib.ls_kernel_resources(b"no_such_kernel", 2, 6, 0, 0, ctypes.byref(r)) == 1
+    assert "unknown kernel" in lib.ls_last_error().decode()
+    assert lib.ls_kernel_resources(b"paged_decode_fp16", 0, 6, 0, 0, ctypes.byref(r)) == 1
+    assert lib.ls_kernel_resources(b"page_index", 2, 17, 0, 0, ctypes.byref(r)) == 1
+    assert lib.ls_kernel_resources(b"page_index", 2, 6, 0, 0, None) == 1
+

@@ -14,7 +14,9 @@ permutation of the pool; the C oracle runs on the host's cores (OpenMP).
 * C4 INT8 B16 x 16384: N(0,1) fp16 quantised on the GPU by
   ls_int8_finalize_blocks (K) and ls_int8_decode_write (V), codes and scales
   bit-exact against the oracle's quantizers, the last page of K in the fp16
-  residual, output against the oracle over the INT8 cache.
+  residual, output against the oracle over the INT8 cache; and the same
+  quantizers byte-equal to the reference cache's own torch ops run on the
+  GPU, symmetric and asymmetric.
 * C5 sparse 50 % B8 x 32768, and C5h the same at the headline B16 x 16384:
   page bounds bit-exact, page scores against the oracle, the GPU selection
   as sets against the oracle's stable top-k (swaps allowed only inside
@@ -158,6 +160,82 @@ def test_c4_int8_b16x16k_quantised_on_the_gpu():
         got = hip_decode(Q, kq, vq, T, L, 16384, splits, k_scale=ks, v_scale=vs,
                          k_residual=R, res_rows=RR)
         assert_close(got, want, ATOL, RTOL, f"c4 splits={splits}")
+
+
+@pytest.mark.parametrize("asym", [False, True])
+def test_c4_quantizers_equal_the_references_torch_ops_on_the_gpu(asym):
+    """At C4's full size, the HIP quantizers against the reference cache's
+    own torch op sequence run on the same GPU tensors (the computation its
+    cache executes on a GPU): Int8PagedKVCache._finalize_blocks for K per
+    (block, head, channel) and the decode write's V per (token, head),
+    cache/int8_paged_cache.py:683-699 and :741-758.  Codes, steps and zero
+    points byte-equal."""
+    from latentserve_amd.kernels.hip import int8_write as iw
+
+    print(f"c4: quantizers against torch on the GPU, asym={asym}", flush=True)
+    _, k16, v16, _, _ = config_case([16384] * 16, seed=44)
+    nb = k16.shape[0]
+    K16, V16 = dev(k16, v16)
+    eps, qmax, levels, offset = 1e-8, 127, 255, 128        # the reference's constants
+    # ---- the reference's ops, on the GPU ----
+    f = K16.to(torch.float32)
+    if asym:
+        lo, hi = f.amin(dim=1), f.amax(dim=1)
+        step = ((hi - lo) / levels).clamp_min(eps)
+        q_u = torch.clamp(torch.round((f - lo.unsqueeze(1)) / step.unsqueeze(1)), 0, levels)
+        want_kq = (q_u - offset).to(torch.int8)
+        want_kz = lo + offset * step
+    else:
+        step = f.abs().amax(dim=1).clamp_min(eps) / qmax
+        want_kq = torch.clamp(torch.round(f / step.unsqueeze(1)), -qmax, qmax).to(torch.int8)
+    want_ks = step
+    del f
+    vf = V16.to(torch.float32)
+    if asym:
+        v_lo = vf.amin(dim=-1, keepdim=True)
+        v_hi = vf.amax(dim=-1, keepdim=True)
+        v_step = ((v_hi - v_lo) / levels).clamp_min(eps)
+        v_u = torch.clamp(torch.round((vf - v_lo) / v_step), 0, levels)
+        want_vq = (v_u - offset).to(torch.int8)
+        want_vz = (v_lo + offset * v_step).squeeze(-1)
+        del v_u
+    else:
+        v_step = vf.abs().amax(dim=-1, keepdim=True).clamp_min(eps) / qmax
+        want_vq = torch.clamp(torch.round(vf / v_step), -qmax, qmax).to(torch.int8)
+    want_vs = v_step.squeeze(-1)
+    del vf
+    # ---- the HIP quantizers ----
+    qargs = dict(asym=asym, eps=float(eps), qmax=float(qmax), levels=float(levels),
+                 offset=float(offset))
+    kq = torch.empty(k16.shape, dtype=torch.int8, device="cuda")
+    ks = torch.empty(nb, H_KV, D, dtype=torch.float32, device="cuda")
+    kz = torch.empty_like(ks) if asym else None
+    iw.finalize_blocks(K16, torch.arange(nb, device="cuda"), kq, ks, k_zero=kz, **qargs)
+    ntok = nb * PAGE
+    vq = torch.empty(ntok, H_KV, D, dtype=torch.int8, device="cuda")
+    vs = torch.empty(ntok, H_KV, dtype=torch.float32, device="cuda")
+    vz = torch.empty_like(vs) if asym else None
+    k_res_dummy = torch.empty(1, H_KV, D, dtype=torch.float16, device="cuda")
+    iw.decode_write(K16.view(ntok, H_KV, 1, D), V16.view(ntok, H_KV, 1, D),
+                    torch.arange(ntok, device="cuda"),
+                    torch.full((ntok,), -1, dtype=torch.long, device="cuda"),
+                    vq, vs, vz, k_res_dummy, **qargs)
+    torch.cuda.synchronize()
+
+    def same_bits(a, b, what):
+        a, b = a.contiguous().view(-1), b.contiguous().view(-1)
+        if a.dtype == torch.float32:
+            a, b = a.view(torch.int32), b.view(torch.int32)
+        bad = int((a != b).sum().item())
+        assert bad == 0, f"{what}: {bad} of {a.numel()} differ"
+
+    same_bits(kq, want_kq, "K codes")
+    same_bits(ks, want_ks, "K steps")
+    same_bits(vq.view(want_vq.shape), want_vq, "V codes")
+    same_bits(vs.view(want_vs.shape), want_vs, "V steps")
+    if asym:
+        same_bits(kz, want_kz, "K zero points")
+        same_bits(vz.view(want_vz.shape), want_vz, "V zero points")
 
 
 def _sets_agree(got_sel, want_sel, scores, what):

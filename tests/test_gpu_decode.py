@@ -44,7 +44,7 @@ def run_fp16(case, num_splits=None, max_len=None):
 
 def test_library_is_the_hip_build():
     from latentserve_amd import _lib
-    assert _lib.lib().ls_abi_version() == _lib.ABI_VERSION == 18
+    assert _lib.lib().ls_abi_version() == _lib.ABI_VERSION == 19
 
 
 @pytest.mark.parametrize("splits", [None, 1, 3, 64])
@@ -336,3 +336,40 @@ def test_any_max_seq_len_gives_the_same_result(max_len):
     for splits in (1, 5, 16):
         assert_close(run_fp16(case, splits, max_len=max_len), want, ATOL, RTOL,
                      f"max_len={max_len} splits={splits}")
+
+
+def test_kernel_resources_report_no_spills():
+    """Every decode and page-subset kernel as the runtime loaded it
+    (kernel_resources, the reference's kernels/cuda/paged_decode_cuda.py:
+    163-186 and paged_sparse.py:254-265): no private (spill) memory, and the
+    decode walks fit one workgroup of 8 waves (paired heads) a CU."""
+    from latentserve_amd.kernels.hip import paged_decode_hip as pdh
+    from latentserve_amd.kernels.hip import paged_sparse as ps
+    seen = {}
+    for variant, asym, res in (("fp16", False, False), ("int8", False, False),
+                               ("int8", False, True), ("int8", True, False), ("int8", True, True)):
+        for heads in (2, 3):
+            r = pdh.kernel_resources(variant=variant, asym=asym, has_res=res, kv_heads=heads,
+                                     min_blocks=12)
+            seen[(variant, asym, res, heads)] = r
+            assert r["local_bytes"] == 0, (variant, asym, res, heads, r)
+            assert r["groups_per_cu"] >= 1 and r["threads"] == (512 if heads == 2 else 256), r
+            assert r["regs"] <= 256 and r["shared_bytes"] <= 160 * 1024, r
+    for name, r in ps.kernel_resources().items():
+        assert r["local_bytes"] == 0, (name, r)
+        assert r["groups_per_cu"] >= 1, (name, r)
+    print(seen)
+
+
+def test_paged_decode_cuda_name_ignores_min_blocks():
+    """The reference's launcher name and signature (min_blocks accepted):
+    the same kernel as paged_decode_hip, against the oracle (the waves
+    claim pages dynamically, so two calls may differ in the last bit)."""
+    from latentserve_amd.kernels.hip import paged_decode_hip as pdh
+    case = paged_case([700, 33, 2048], seed=9)
+    want = oracle.paged_decode(*case)
+    Q, K, V, T, L = dev(*case)
+    for mb in (None, 1, 12):
+        got = pdh.paged_decode_cuda(Q, K, V, T, L, 2048, num_splits=4, min_blocks=mb)
+        assert_close(got.float().cpu().numpy(), want, ATOL, RTOL, f"min_blocks={mb}")
+

@@ -51,6 +51,38 @@ def test_block_table_slot_rule():
     assert t.version == v + 1 and len(t.blocks) == 4
 
 
+def test_allocator_stats_and_reset_follow_the_reference():
+    """stats() under the reference's keys, reset() clearing the peak and the
+    call counts as well (cache/block_allocator.py:147-161)."""
+    a = BlockAllocator(num_blocks=8, block_size=16)
+    a.allocate(5)
+    a.free([4, 3])
+    a.allocate(1)
+    st = a.stats()
+    assert st == {"num_blocks": 8, "block_size": 16, "blocks_used": 4, "blocks_free": 4,
+                  "block_utilization": 0.5, "peak_blocks_used": 5, "alloc_calls": 2,
+                  "free_calls": 1}
+    a.reset()
+    assert a.stats()["peak_blocks_used"] == 0 and a.alloc_calls == 0 and a.free_calls == 0
+    assert a.allocate(2) == [0, 1]
+
+
+def test_block_table_capacity_wasted_slots_and_reserve():
+    """capacity / wasted_slots / reserve as the reference's BlockTable
+    (cache/block_allocator.py:190-212): reserve allocates pages for tokens
+    to come without counting them."""
+    a = BlockAllocator(num_blocks=10, block_size=16)
+    t = BlockTable(a)
+    t.reserve(20)
+    assert t.length == 0 and t.capacity == 32 and t.wasted_slots == 32 and t.version == 1
+    t.append(20)                            # the reserved pages suffice
+    assert t.blocks == [0, 1] and t.version == 1 and t.wasted_slots == 12
+    t.reserve(12)
+    assert t.version == 1 and t.capacity == 32
+    t.reserve(13)
+    assert t.version == 2 and t.capacity == 48 and t.length == 20
+
+
 def _cache(batch=3, cap=100, layers=2):
     spec = KVCacheSpec(num_layers=layers, num_kv_heads=2, head_dim=128, max_batch_size=batch,
                        max_seq_len=cap, device="cpu")
