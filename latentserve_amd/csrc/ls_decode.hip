@@ -34,7 +34,9 @@
 //    does, paged_decode_int8.cu:230-242).  The sequence's last page takes K
 //    from the fp16 residual (paged_decode.py:213-216).
 //  * Page prefetch: the next page's K/V (and scales) are issued before the
-//    current page is computed (two register buffers).
+//    current page is computed (two buffers).  fp16 K rows go through LDS
+//    (whole-line direct loads into a per-wave slot, read back in the MFMA
+//    layout), V and every INT8 row straight to registers.
 //  * Splits: NW waves merge in LDS; with more than one split, every group
 //    writes its (acc, m, l) record (acc [NR][128] as the reference's
 //    partials hold it, then each row's m, in natural-log units as the
