@@ -417,6 +417,8 @@ def timeline(cfg, args):
     lib = ctypes.CDLL(os.environ["LATENTSERVE_HIP_LIB"])
     buf = np.zeros(8192 * 16, np.uint64)
     rel, xcd_ok, groups = [], 0, 0
+    spread = {"launch_end": [], "max_minus_median": [], "xcd_median_range": [],
+              "within_xcd_range_median": []}
     for _ in range(8):
         for c in calls:
             c()
@@ -431,9 +433,28 @@ def timeline(cfg, args):
         rel.append(np.where(s >= base, (s - base) * 0.01, np.nan))
         xcd_ok += int(((last % 8) == (st[last, 15] & 15)).sum())
         groups += len(last)
+        # where the groups' merge times spread: between XCDs or within one
+        merged = (st[last, 9] - base) * 0.01
+        xcd = st[last, 15] & 15
+        ok = st[last, 9] >= base
+        if ok.any():
+            m, x = merged[ok], xcd[ok]
+            meds = [float(np.median(m[x == k])) for k in range(8) if (x == k).any()]
+            rngs = [float(np.ptp(m[x == k])) for k in range(8) if (x == k).sum() > 1]
+            spread["launch_end"].append(float(m.max()))
+            spread["max_minus_median"].append(float(m.max() - np.median(m)))
+            spread["xcd_median_range"].append(max(meds) - min(meds))
+            spread["within_xcd_range_median"].append(float(np.median(rngs)) if rngs else 0.0)
+            spread.setdefault("xcd_medians", []).append(
+                [round(float(np.median(m[x == k])), 1) if (x == k).any() else None
+                 for k in range(8)])
     rel = np.concatenate(rel)
     out = {"config": cfg["workload"], "launches": 8, "groups": groups,
-           "groups_on_xcd_L_mod_8": xcd_ok, "us_from_first_group_start": {}}
+           "groups_on_xcd_L_mod_8": xcd_ok, "us_from_first_group_start": {},
+           "merge_spread_us (median over launches)": {
+               k: round(float(np.median(v)), 2) for k, v in spread.items()
+               if v and k != "xcd_medians"},
+           "xcd_median_merge_us_per_launch": spread.get("xcd_medians", [])}
     order = [0, 1, 2, 3, 4, 13, 14, 5, 6, 7, 8, 9, 10, 11, 12]
     for i in order:
         col = rel[:, i]
@@ -472,7 +493,8 @@ def main():
     nbytes = algorithmic_bytes(cfg, lens)
     from latentserve_amd.kernels.hip import paged_decode_hip as pdh
     splits = args.splits or pdh.choose_splits(cfg["batch"], H_KV, (max_len + PAGE - 1) // PAGE,
-                                              torch.device("cuda", 0))
+                                              torch.device("cuda", 0),
+                                              int8=cfg["kind"] == "int8")
     calls = [make_call(cfg, tables, seq, pools[i], max_len, splits) for i in range(layers)]
 
     for i in range(args.warmup):

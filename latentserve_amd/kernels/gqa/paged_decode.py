@@ -48,11 +48,12 @@ def decode_backend() -> str:
 
 
 def choose_num_splits(batch: int, kv_heads: int, max_seq_len: int, page: int,
-                      device: torch.device) -> int:
+                      device: torch.device, int8: bool = False) -> int:
     """The split rule ``paged_decode_attention`` applies when ``num_splits`` is
-    None, callable before a launch so a graph runner can pin it per bucket."""
+    None, callable before a launch so a graph runner can pin it per bucket
+    (``int8``: for an INT8 pool)."""
     num_pages = (max_seq_len + page - 1) // page
-    return hip.choose_splits(batch, kv_heads, num_pages, device)
+    return hip.choose_splits(batch, kv_heads, num_pages, device, int8=int8)
 
 
 def combine_splits(partial_acc: torch.Tensor, partial_m: torch.Tensor, partial_l: torch.Tensor,

@@ -26,11 +26,15 @@ HEAD_DIM = 128
 PAGE = 16
 MAX_NREP = 16
 MAX_SPLITS = 1024
-# (sequence, KV head, split) units per CU the split count aims at: the fp16
-# kernel runs one workgroup per split of a KV-head pair, so two units a CU is
-# one workgroup per CU, the measured optimum (more groups than CUs leaves a
-# second, partial round).
-UNITS_PER_CU = 2
+# (sequence, KV head, split) units per 4 CUs the split count aims at.  A
+# workgroup serves the splits of a KV-head pair (two units), one workgroup a
+# CU fits, and more groups than CUs leave a second, partial round.  INT8: one
+# group a CU (8 units a 4 CUs), the measured optimum (B16 x 16K: 14 splits
+# 34.6 us, 15: 33.1, 16: 32.9).  fp16: 7 groups an 8 CUs (7 units a 4 CUs):
+# fewer split records to combine, and the walk is bound by HBM as a whole,
+# not by the CUs (B16 x 16K: 13-14 splits 46.4-46.5 us against 46.7-46.8 at
+# 16; B8 x 32K: 28 splits 48.4 us against 48.8 at 32).
+UNITS_PER_4_CUS = {"fp16": 7, "int8": 8}
 # Fewest pages a split is given.
 MIN_SPLIT_PAGES = 8
 
@@ -45,15 +49,17 @@ def _cus(device: torch.device) -> int:
 
 
 def choose_splits(batch: int, kv_heads: int, num_pages: int,
-                  device: Optional[torch.device] = None) -> int:
+                  device: Optional[torch.device] = None, int8: bool = False) -> int:
     """Splits per (sequence, KV head) for the MI355X kernel.
 
-    Enough (sequence, head, split) units for UNITS_PER_CU per CU, never a
-    split of fewer than MIN_SPLIT_PAGES pages.  Fixed by (batch, heads,
-    pages) alone, so a captured graph can pin it per context bucket.
+    Enough (sequence, head, split) units for UNITS_PER_4_CUS per 4 CUs (the
+    fp16 or the INT8 walk's), never a split of fewer than MIN_SPLIT_PAGES
+    pages.  Fixed by (batch, heads, pages, pool type) alone, so a captured
+    graph can pin it per context bucket.
     """
     cus = _cus(device) if device is not None and torch.cuda.is_available() else 256
-    by_cus = -(-(UNITS_PER_CU * cus) // max(1, batch * kv_heads))
+    units = UNITS_PER_4_CUS["int8" if int8 else "fp16"] * cus // 4
+    by_cus = -(-units // max(1, batch * kv_heads))
     by_pages = max(1, num_pages // MIN_SPLIT_PAGES)
     return max(1, min(MAX_SPLITS, by_cus, by_pages))
 
@@ -174,7 +180,8 @@ def paged_decode_hip(q, k_pool, v_pool, block_tables, seq_lens, max_seq_len: int
     _check_common(q, k_pool, v_pool, block_tables, seq_lens)
     b, h_kv, n_rep, d = q.shape
     num_pages = -(-int(max_seq_len) // PAGE)
-    splits = int(num_splits) if num_splits else choose_splits(b, h_kv, num_pages, q.device)
+    splits = int(num_splits) if num_splits else choose_splits(b, h_kv, num_pages, q.device,
+                                                              int8=k_pool.dtype == torch.int8)
     splits = max(1, min(MAX_SPLITS, splits))
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
     is_int8 = k_pool.dtype == torch.int8

@@ -171,7 +171,7 @@ class GraphedDecoder:
 
         c = self.model.cache
         return choose_num_splits(batch, c.spec.num_kv_heads, bucket, c.block_size,
-                                 self.model.device)
+                                 self.model.device, int8=c.k_pool[0].dtype == torch.int8)
 
     def _ratio_for_step(self, slots: Sequence[int]) -> Optional[float]:
         """The sparse ratio of this step: the policy's choice at the batch's
