@@ -192,6 +192,18 @@ __device__ __forceinline__ T load_coherent(const T* p) {
 // is not tracked: with an explicit wait after it the compiler still took
 // the asm's outputs as ready at once, and reading m and l of the records
 // that way gave wrong results.)
+// A pointer that is the same in every lane of the wave, declared so: the
+// compiler otherwise keeps a value derived from threadIdx (a head of the
+// group, say) in vector registers, and a buffer resource built from it
+// becomes a loop of one-lane-group loads, each waiting for the one before.
+template <class T>
+__device__ __forceinline__ T* wave_uniform(T* p) {
+    const uint64_t x = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+    return (T*)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const float* base) {
     // (dword 3: the raw-buffer format bits CDNA's buffer instructions expect)
     return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, 0x7fffffff, 0x00020000);
@@ -201,6 +213,16 @@ __device__ __forceinline__ f4 load_coherent4(__amdgpu_buffer_rsrc_t rs, int byte
     // read once: 0.05 us faster at B16 x 16K than sc1 alone)
     constexpr int POLICY = 16 | 2;
     return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, POLICY));
+}
+
+// (soff: a wave-uniform byte offset, in a scalar register)
+__device__ __forceinline__ f4 load_coherent4(__amdgpu_buffer_rsrc_t rs, int byte_off, int soff) {
+    constexpr int POLICY = 16 | 2;
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, soff, POLICY));
+}
+__device__ __forceinline__ uint64_t load_coherent8(__amdgpu_buffer_rsrc_t rs, int byte_off, int soff) {
+    constexpr int POLICY = 16 | 2;
+    return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rs, byte_off, soff, POLICY));
 }
 
 // Workgroup ids renumbered XCD-major.  The dispatcher deals a launch's

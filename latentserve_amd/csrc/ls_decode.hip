@@ -379,9 +379,8 @@ __device__ __forceinline__ void store_coherent2(float* p, float x, float y) {
     asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
 
-// VEC 4: 16-byte loads; 1: scalar loads; 0: device-coherent loads of the
-// fused decode's records (written by other workgroups of the same launch;
-// m and l of a row side by side at m + 2 r, `l` unused).
+// The standalone split merge (ls_combine_splits): VEC 4, 16-byte loads; 1,
+// scalar loads.
 template <int VEC>
 __device__ void combine_partials(const float* acc, const float* m, const float* l, int S, int NR,
                                  int64_t sa_s, int64_t sa_r, int64_t sm_s, void* out, int out_f32,
@@ -390,14 +389,9 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
         const int r = o / (HEAD_DIM / 4), d0 = (o % (HEAD_DIM / 4)) * 4;
         float mg = neg_inf(), lt = 0.f;
         float at[4] = {0.f, 0.f, 0.f, 0.f};
-        // VEC 0: the records through a buffer resource, so the 16-byte
-        // device-coherent (sc1) loads are ones the compiler waits for
-        const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(acc);
         for (int s0 = 0; s0 < S; s0 += CMB_CHUNK) {
             const int n = S - s0 < CMB_CHUNK ? S - s0 : CMB_CHUNK;
             float mv[CMB_CHUNK], lv[CMB_CHUNK], av[CMB_CHUNK][4];
-            f4 avc[CMB_CHUNK];
-            uint64_t mlc[CMB_CHUNK];
             // Every slot loads (slots past the last split reread it) and is
             // masked afterwards: loads under a branch would each wait for
             // the one before.
@@ -405,14 +399,6 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
             for (int i = 0; i < CMB_CHUNK; ++i) {
                 const int64_t sp = s0 + i < S ? s0 + i : S - 1;
                 const float* src = acc + sp * sa_s + r * sa_r + d0;
-                if (VEC == 0) {
-                    // (m and l as one relaxed 8-byte atomic load: sc1, and
-                    // the compiler tracks its wait)
-                    mlc[i] = __hip_atomic_load((const uint64_t*)(m + sp * sm_s + 2 * r),
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    avc[i] = load_coherent4(rs, (int)((src - acc) * sizeof(float)));
-                    continue;
-                }
                 mv[i] = m[sp * sm_s + r];
                 lv[i] = l[sp * sm_s + r];
                 if (VEC == 4) {
@@ -422,15 +408,6 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) av[i][e] = src[e];
-                }
-            }
-            if (VEC == 0) {
-#pragma unroll
-                for (int i = 0; i < CMB_CHUNK; ++i) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) av[i][e] = avc[i][e];
-                    mv[i] = __builtin_bit_cast(float, (uint32_t)mlc[i]);
-                    lv[i] = __builtin_bit_cast(float, (uint32_t)(mlc[i] >> 32));
                 }
             }
 #pragma unroll
@@ -468,6 +445,74 @@ __device__ void combine_partials(const float* acc, const float* m, const float* 
             else
                 ((half_t*)out)[r * so_r + d0 + e] = (half_t)v;
         }
+    }
+}
+
+// The fused decode's split merge over its records (write-through, read with
+// device-coherent loads): per split s the accumulator rows at
+// acc + s * sa_s + r * sa_r, and m (natural-log units) and l of row r side by
+// side at m + s * sm_s + 2r.  Lane j of each half-wave takes channels
+// 4j..4j+4 of one row r, and loads m and l of split j of the round: the
+// round's weights exp(m_s - m_max) are computed once a split and handed to
+// the other lanes by readlane, so a lane holds R accumulator records and no
+// other, and up to R (16 or 32) splits are merged in one memory round trip.
+// 256 threads, fp16 out.
+template <int R>
+__device__ void combine_records(const float* acc, const float* m, int S, int NR, int64_t sa_s,
+                                int64_t sa_r, int64_t sm_s, half_t* out, int64_t so_r, int tid) {
+    static_assert(R == 16 || R == 32, "a round is at most a half-wave of splits");
+    // (acc and S are the same in every lane of the wave: declared so, the
+    // resource and the split offsets are scalar and the loads issue together)
+    S = __builtin_amdgcn_readfirstlane(S);
+    const __amdgpu_buffer_rsrc_t rs = coherent_rsrc(wave_uniform(acc));
+    const int j = tid & 31;
+    const bool upper = (tid & 32) != 0;
+    for (int o = tid; o < NR * 32; o += 256) {
+        const int r = o / 32, d0 = 4 * j;
+        float mg = neg_inf(), lt = 0.f;
+        f4 at = {0.f, 0.f, 0.f, 0.f};
+        const int vo_m = (int)(((m - acc) + 2 * r) * (int64_t)sizeof(float));
+        const int vo_a = (int)((r * sa_r + d0) * (int64_t)sizeof(float));
+        for (int s0 = 0; s0 < S; s0 += R) {
+            const int n = S - s0 < R ? S - s0 : R;      // the same in every lane
+            // Every slot loads (slots past the last split reread it) and is
+            // weighted 0: loads under a branch would each wait for the one
+            // before.  The split's offset is wave-uniform, a scalar operand.
+            const int sj = s0 + (j < n ? j : n - 1);     // (lanes j >= R weigh 0)
+            const uint64_t ml = load_coherent8(rs, vo_m + (int)(sj * sm_s * (int64_t)sizeof(float)), 0);
+            f4 av[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int sp = s0 + (i < n ? i : n - 1);
+                av[i] = load_coherent4(rs, vo_a, (int)(sp * sa_s * (int64_t)sizeof(float)));
+            }
+            const float mj = j < n ? __builtin_bit_cast(float, (uint32_t)ml) : neg_inf();
+            float cm = mj;
+#pragma unroll
+            for (int k = 16; k > 0; k >>= 1) cm = fmaxf(cm, shfl_xor(cm, k));
+            cm = fmaxf(cm, mg);                     // the same in the half-wave
+            const bool none = cm == neg_inf();      // nothing valid yet
+            const float sc = none ? 1.f : __expf(mg - cm);          // 0 while mg is -inf
+            const float wj = none || j >= n ? 0.f : __expf(mj - cm);  // 0 for empty splits
+            float lj = wj * __builtin_bit_cast(float, (uint32_t)(ml >> 32));
+#pragma unroll
+            for (int k = 16; k > 0; k >>= 1) lj += shfl_xor(lj, k);
+            lt = lt * sc + lj;
+            at *= sc;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const float w0 = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), i));
+                const float w1 = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), 32 + i));
+                at += av[i] * (upper ? w1 : w0);
+            }
+            mg = none ? mg : cm;
+        }
+        const float inv = 1.f / fmaxf(lt, 1e-20f);
+        half_t* op = out + r * so_r + d0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) op[e] = (half_t)(at[e] * inv);
     }
 }
 
@@ -1342,10 +1387,15 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     {
         // device-coherent loads: the records of groups on other XCDs
         const float* recs = a.work + ((int64_t)gw.first * H + h0 + hh) * rec;
-        combine_partials<0>(recs, recs + NR * HEAD_DIM, nullptr, Sb, NR,
-                            (int64_t)H * rec, HEAD_DIM, (int64_t)H * rec,
-                            a.out + (int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h, 0, a.so_r,
-                            t256);
+        // (a round of 32 slots for 16 splits or fewer would reread the
+        // last split's record 16 times and more: c2 +1.6 us)
+        half_t* o = a.out + (int64_t)b * a.so_b + (int64_t)(h0 + hh) * a.so_h;
+        if (Sb <= 16)
+            combine_records<16>(recs, recs + NR * HEAD_DIM, Sb, NR, (int64_t)H * rec, HEAD_DIM,
+                                (int64_t)H * rec, o, a.so_r, t256);
+        else
+            combine_records<32>(recs, recs + NR * HEAD_DIM, Sb, NR, (int64_t)H * rec, HEAD_DIM,
+                                (int64_t)H * rec, o, a.so_r, t256);
     }
     LS_STAMP(12);
     // every group of this (b, h) has arrived: back to zero for the next launch
