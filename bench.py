@@ -455,12 +455,16 @@ def timeline(cfg, args):
                k: round(float(np.median(v)), 2) for k, v in spread.items()
                if v and k != "xcd_medians"},
            "xcd_median_merge_us_per_launch": spread.get("xcd_medians", [])}
-    order = [0, 1, 2, 3, 4, 13, 14, 5, 6, 7, 8, 9, 10, 11, 12]
+    order = ([0, 1, 2, 3, 4, 13, 14, 5, 6, 7, 8, 9, 10, 11, 12] if cfg["kind"] == "sparse"
+             else [0, 8, 1, 2, 9, 10, 11, 12])
     for i in order:
         col = rel[:, i]
         col = col[~np.isnan(col)]
         if len(col):
-            out["us_from_first_group_start"][STAMP_NAMES[i]] = {
+            name = STAMP_NAMES[i]
+            if cfg["kind"] != "sparse" and i in (1, 2):
+                name = {1: "first wave's walk end", 2: "last wave's walk end"}[i]
+            out["us_from_first_group_start"][name] = {
                 "groups": int(len(col)), "p10": round(float(np.percentile(col, 10)), 2),
                 "median": round(float(np.median(col)), 2),
                 "p90": round(float(np.percentile(col, 90)), 2), "max": round(float(col.max()), 2)}

@@ -802,7 +802,10 @@ __device__ float score_one(const DecodeParams& a, int b, int h, int len, int p) 
 // 3 the same with the scores computed by the launch itself, each group
 // scoring its share of its sequence's pages (score_slice).
 template <int KIND, bool ASYM, bool HAS_RES, int SPARSE, int NWT, int HG, int ABL = 0>
-__global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodeParams a) {
+// (two waves a SIMD also for the 4-wave groups of odd head counts: the
+// register budget of the 8-wave groups, 256)
+__global__ __launch_bounds__(WAVE* NWT) __attribute__((amdgpu_waves_per_eu(2)))
+void paged_decode_kernel(const DecodeParams a) {
     // Pages in flight ahead of the one being computed: one.  INT8: a second
     // buffer measured slower (c4 35.3 -> 39.1 us; with the page loads as
     // inline asm and the walk's own waits, 37.5 us at one head a group,
@@ -852,9 +855,13 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // Each head of the group has its own NWH waves (wave wv serves head hw
     // of the pair as its wl-th wave): a wave holds one head's state and
     // query, and both heads' waves walk the same pages at about the same
-    // time, so the two halves of a token row are still read together.
+    // time, so the two halves of a token row are still read together.  The
+    // heads alternate over the waves: the older waves win memory
+    // arbitration, and with the first half of the waves on one head that
+    // head ran ahead and its waves idled while the other's finished (c4
+    // 32.60 -> 32.30, c2 46.15 -> 45.89, s8k 27.14 -> 26.97 us).
     constexpr int NWH = NWT / HG;
-    const int hw = wv / NWH, wl = wv % NWH;
+    const int hw = wv % HG, wl = wv / HG;
     if (threadIdx.x < (unsigned)HG) sm.claim[threadIdx.x] = NB * NWH;   // below: fixed items
 
     // Dense walk with pages-per-split given by the host (from the caller's
@@ -1268,6 +1275,12 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
     // the wave's slots; none may land after the group ends)
     if constexpr (KIND == KV_FP16) wait_vm_lds<0>();
     LS_STAMP(8);
+#ifdef LS_STAMPS
+    // (dense walks: the first and the last of the group's waves to end their
+    // walks, stamps 1 and 2, recorded after the merge's barrier)
+    __shared__ uint64_t wave_end[NWT];
+    if (lane == 0) wave_end[wv] = __builtin_amdgcn_s_memrealtime();
+#endif
 
     const int NR = a.NR;
     const bool single = Sb == 1;
@@ -1364,6 +1377,17 @@ __global__ __launch_bounds__(WAVE* NWT) void paged_decode_kernel(const DecodePar
         }
     }
     LS_STAMP(9);
+#ifdef LS_STAMPS
+    if (!SPARSE && threadIdx.x == 0) {
+        uint64_t lo = wave_end[0], hi = wave_end[0];
+        for (int w = 1; w < NWT; ++w) {
+            lo = wave_end[w] < lo ? wave_end[w] : lo;
+            hi = wave_end[w] > hi ? wave_end[w] : hi;
+        }
+        g_ls_stamps[(blockIdx.x + gridDim.x * blockIdx.y) * LS_NSTAMP + 1] = lo;
+        g_ls_stamps[(blockIdx.x + gridDim.x * blockIdx.y) * LS_NSTAMP + 2] = hi;
+    }
+#endif
     if (single) return;
 
     // ---- the last group of each (b, h) to arrive merges all splits ----
