@@ -415,7 +415,7 @@ def timeline(cfg, args):
             c()
     torch.cuda.synchronize()
     lib = ctypes.CDLL(os.environ["LATENTSERVE_HIP_LIB"])
-    buf = np.zeros(8192 * 16, np.uint64)
+    buf = np.zeros(8192 * 32, np.uint64)
     rel, xcd_ok, groups = [], 0, 0
     spread = {"launch_end": [], "max_minus_median": [], "xcd_median_range": [],
               "within_xcd_range_median": []}
@@ -425,7 +425,7 @@ def timeline(cfg, args):
         torch.cuda.synchronize()
         assert lib.ls_diag_read_stamps(buf.ctypes.data_as(ctypes.c_void_p),
                                        ctypes.c_size_t(buf.nbytes)) == 0
-        st = buf.reshape(8192, 16).astype(np.int64)
+        st = buf.reshape(8192, 32).astype(np.int64)
         t0 = st[:, 0]
         last = np.where(t0 > t0.max() - 10000)[0]          # the last launch's groups
         base = st[last, 0].min()

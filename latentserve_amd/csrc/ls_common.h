@@ -23,7 +23,7 @@ constexpr int WAVE = 64;
 // of each workgroup records the 100 MHz clock at numbered points of the
 // decode (ls_diag_read_stamps copies the last launch's to the host).
 #ifdef LS_STAMPS
-constexpr int LS_NSTAMP = 16;
+constexpr int LS_NSTAMP = 32;   // 0-15: the group's points; 16-31: per wave (dense walks)
 static __device__ uint64_t g_ls_stamps[8192 * LS_NSTAMP];
 #define LS_STAMP(i)                                                                              \
     do {                                                                                         \

@@ -1196,6 +1196,9 @@ void paged_decode_kernel(const DecodeParams a) {
         return it < n_items && blk >= 0 && blk < a.num_blocks && pg >= 0 && pg < num_pages &&
                !(HAS_RES && pg == num_pages - 1 && !res_ok);
     };
+#ifdef LS_STAMPS
+    int n_done = 0;     // items this wave computed live
+#endif
     auto walk = [&](auto resolve, auto first) {
         if constexpr (HAS_RES) {
             // the last wave of each head computes that head's last page
@@ -1246,6 +1249,9 @@ void paged_decode_kernel(const DecodeParams a) {
                 // force conservative waits on the next reuse of its registers
                 const bool ok_u = live(u);
                 const int live_len = ok_u ? len : 0;
+#ifdef LS_STAMPS
+                n_done += ok_u ? 1 : 0;
+#endif
                 k_from_lds(u);
                 if (ABL == 1 || ABL == 2)
                     consume_page<KIND>(buf[u], st);
@@ -1279,7 +1285,15 @@ void paged_decode_kernel(const DecodeParams a) {
     // (dense walks: the first and the last of the group's waves to end their
     // walks, stamps 1 and 2, recorded after the merge's barrier)
     __shared__ uint64_t wave_end[NWT];
-    if (lane == 0) wave_end[wv] = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) {
+        wave_end[wv] = __builtin_amdgcn_s_memrealtime();
+        // per wave (up to 8): walk end, and items computed | head << 16
+        if (wv < 8) {
+            uint64_t* ws = g_ls_stamps + (blockIdx.x + gridDim.x * blockIdx.y) * LS_NSTAMP + 16;
+            ws[wv] = wave_end[wv];
+            ws[8 + wv] = (uint64_t)(n_done | (hw << 16));
+        }
+    }
 #endif
 
     const int NR = a.NR;
