@@ -687,15 +687,15 @@ __device__ __forceinline__ int claimed_item(int raw) { return __builtin_amdgcn_r
 // group's HG heads, stored write-through into a.scores (the index kernel's
 // rule: page 0 and the last `recent` pages +inf, pages past the end or with
 // a block id outside the pool -inf).  Each 16-lane row of a wave takes one
-// (page, head) unit a round, 8 channels a lane; the block ids of up to
-// four rounds are requested together, then their bounds.
-template <int NWT, int HG>
+// (page, head) unit a round, 8 channels a lane; the block ids of R rounds
+// are requested together, then their bounds (two dependent round trips a
+// batch of R rounds: the caller picks R so that its share is one batch).
+template <int NWT, int HG, int R>
 __device__ void score_slice(const DecodeParams& a, int b, int h0, int len, int p_lo, int p_hi) {
     const int lane = threadIdx.x % WAVE, wv = threadIdx.x / WAVE;
     const int row = lane >> 4, c0 = (lane & 15) * 8;
     const int np = len > 0 ? (len + PAGE - 1) / PAGE : 0;
     constexpr int PPR = 4 / HG;                 // pages a wave takes a round
-    constexpr int R = 4;                        // rounds requested together
     const int hh = row % HG;
     const half_t* qb = a.q + (int64_t)b * a.sq_b + (int64_t)(h0 + hh) * a.sq_h + c0;
     float* srow = a.scores + (int64_t)b * a.ssc_b + (int64_t)(h0 + hh) * a.ssc_h;
@@ -1076,7 +1076,13 @@ void paged_decode_kernel(const DecodeParams a) {
                 const int per = (a.score_pages + Sb - 1) / Sb;
                 const int p_lo = gw.s * per;
                 const int p_hi = p_lo + per < a.score_pages ? p_lo + per : a.score_pages;
-                score_slice<NWT, HG>(a, b, h0, len, p_lo, p_hi);
+                // (shares of up to 64 pages in one batch of 4 rounds, up to
+                // 128 in one of 8: B8 x 32K at 28 splits, 74-page shares,
+                // had taken two batches of 4)
+                if (p_hi - p_lo <= 4 * NWT * (4 / HG))
+                    score_slice<NWT, HG, 4>(a, b, h0, len, p_lo, p_hi);
+                else
+                    score_slice<NWT, HG, 8>(a, b, h0, len, p_lo, p_hi);
                 LS_STAMP(1);
                 // the group's score stores complete, then it counts itself in
                 // the word after row (b, h0) (all ones at rest, so the count
