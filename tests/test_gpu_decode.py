@@ -47,8 +47,10 @@ def test_library_is_the_hip_build():
     assert _lib.lib().ls_abi_version() == _lib.ABI_VERSION == 19
 
 
-@pytest.mark.parametrize("splits", [None, 1, 3, 64])
+@pytest.mark.parametrize("splits", [None, 1, 3, 16, 17, 32, 33, 64])
 def test_ragged_lengths_match_the_oracle(splits):
+    # (16 / 17 and 32 / 33 splits: the edges of the split merge's rounds of
+    # 16 and 32 records; 64: two rounds of 32)
     case = paged_case([1024, 300, 61, 17, 1], seed=0)
     want = oracle.paged_decode(*case, num_splits=1)
     assert_close(run_fp16(case, splits), want, ATOL, RTOL, f"splits={splits}")
