@@ -67,13 +67,18 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=2800)
     p.add_argument("--warmup", type=int, default=280)
-    p.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    p.add_argument("--config", default=None, choices=sorted(CONFIGS),
+                   help="one configuration (default: c2, with the other attention "
+                        "configurations timed after it unless --no-others)")
     p.add_argument("--splits", type=int, default=None)
     p.add_argument("--layers", type=int, default=LAYERS)
     p.add_argument("--tables", default="random", choices=["random", "contiguous"],
                    help="block-table layout (contiguous: the pages of a sequence are adjacent, "
                         "a diagnostic of the gather's cost)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-others", action="store_true",
+                   help="the default run: skip timing the other attention configurations "
+                        "(reported under 'other_configs' of the same line)")
     p.add_argument("--cpu-seqs", type=int, default=None,
                    help="sequences in the CPU-baseline sample (default: the whole batch)")
     p.add_argument("--compute-probe", type=int, default=0, metavar="ITEMS",
@@ -486,17 +491,60 @@ def main():
     if args.compute_probe:
         compute_probe(args.compute_probe, args.diag_lib)
         return
+    default_run = args.config is None
+    args.config = args.config or "c2"
     cfg = CONFIGS[args.config]
     if args.timeline:
         return timeline(cfg, args)
     if cfg["kind"] == "step":
         return bench_step(cfg, args)
+    tables, seq, pools, max_len, splits, nbytes, ms_step = measure(cfg, args)
+    gbps = nbytes / (ms_step * 1e-3) / 1e9
+    layers = max(1, args.layers)
+
+    result = {
+        "metric": "paged-decode attn us/layer-step + HBM GB/s (% of 8 TB/s peak), B16x16K fp16",
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "us_per_layer_step": round(ms_step * 1e3, 3),
+        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 KV / fp16 q" if cfg["kind"] == "int8" else "fp16",
+        "data": "synthetic N(0,1), seeded device generator, permuted block tables",
+        "config": {"workload": cfg["workload"], "batch": cfg["batch"], "ctx": cfg["ctx"],
+                   "kv_heads": H_KV, "n_rep": N_REP, "head_dim": D, "page": PAGE,
+                   "layer_pools": layers, "num_splits": splits,
+                   "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_from_profiles(args.config)},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(cfg, tables, seq, pools[0], args.cpu_seqs)
+    if default_run and not args.no_others and args.splits is None:
+        del tables, seq, pools
+        result["other_configs"] = other_configs(args)
+    print(json.dumps(result))
+
+
+def measure(cfg, args, splits=None):
+    """The layer-step time of one attention configuration: its workload on
+    `args.layers` pools, a graph of `args.steps` launches replayed after
+    `args.warmup` eager ones, HIP events around the replays."""
+    import torch
+
     layers = max(1, args.layers)
     tables, seq, pools, max_len = build_workload(cfg, layers, contiguous=args.tables == "contiguous")
     lens = seq.cpu().numpy()
     nbytes = algorithmic_bytes(cfg, lens)
     from latentserve_amd.kernels.hip import paged_decode_hip as pdh
-    splits = args.splits or pdh.choose_splits(cfg["batch"], H_KV, (max_len + PAGE - 1) // PAGE,
+    splits = splits or args.splits or pdh.choose_splits(cfg["batch"], H_KV, (max_len + PAGE - 1) // PAGE,
                                               torch.device("cuda", 0),
                                               int8=cfg["kind"] == "int8")
     calls = [make_call(cfg, tables, seq, pools[i], max_len, splits) for i in range(layers)]
@@ -533,34 +581,33 @@ def main():
     torch.cuda.synchronize()
     ms = start.elapsed_time(end)
     ms_step = ms / args.steps
-    gbps = nbytes / (ms_step * 1e-3) / 1e9
+    return tables, seq, pools, max_len, splits, nbytes, ms_step
 
-    result = {
-        "metric": "paged-decode attn us/layer-step + HBM GB/s (% of 8 TB/s peak), B16x16K fp16",
-        "value": round(gbps, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 6),
-        "us_per_layer_step": round(ms_step * 1e3, 3),
-        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8 KV / fp16 q" if cfg["kind"] == "int8" else "fp16",
-        "data": "synthetic N(0,1), seeded device generator, permuted block tables",
-        "config": {"workload": cfg["workload"], "batch": cfg["batch"], "ctx": cfg["ctx"],
-                   "kv_heads": H_KV, "n_rep": N_REP, "head_dim": D, "page": PAGE,
-                   "layer_pools": layers, "num_splits": splits,
-                   "algorithmic_bytes_per_step": nbytes},
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_from_profiles(args.config)},
-    }
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(cfg, tables, seq, pools[0], args.cpu_seqs)
-    print(json.dumps(result))
+
+
+def other_configs(args):
+    """The other attention configurations of the configuration table, each
+    measured as the headline is (same steps, warm-up and layer pools) and
+    reported beside it; a configuration that fails is reported with its
+    error and does not stop the run."""
+    import torch
+    out = {}
+    for name in ("c1", "c3", "c3r", "c4", "c5", "c5h", "s8k"):
+        cfg = CONFIGS[name]
+        try:
+            r = measure(cfg, args, splits=None)
+            nb, ms_step = r[5], r[6]
+            gbps = nb / (ms_step * 1e-3) / 1e9
+            out[name] = {"workload": cfg["workload"], "us_per_layer_step": round(ms_step * 1e3, 3),
+                         "algorithmic_gbps": round(gbps, 2),
+                         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "num_splits": r[4],
+                         "algorithmic_bytes_per_step": nb}
+            del r
+        except Exception as e:   # reported, not raised: the headline line still prints
+            out[name] = {"error": f"{type(e).__name__}: {e}"}
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_step(cfg, args):
