@@ -110,10 +110,14 @@ def test_empty_and_tiny_sequences():
     assert_close(got, dense_attention(*case), ATOL, RTOL)
 
 
+@pytest.mark.parametrize("splits", [5, 33])
 @pytest.mark.parametrize("n_rep", [1, 4, 6, 8, 16])
-def test_other_group_sizes(n_rep):
+def test_other_group_sizes(n_rep, splits):
+    # (33 splits: the split merge's rounds of 32 records and a second round,
+    # with the query rows of one to sixteen half-waves)
     case = paged_case([500, 77], n_rep=n_rep, seed=n_rep)
-    assert_close(run_fp16(case, 5), dense_attention(*case), ATOL, RTOL, f"n_rep={n_rep}")
+    assert_close(run_fp16(case, splits), dense_attention(*case), ATOL, RTOL,
+                 f"n_rep={n_rep} splits={splits}")
 
 
 def test_four_kv_heads_and_strided_q():
