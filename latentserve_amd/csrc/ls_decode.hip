@@ -734,6 +734,9 @@ __device__ void score_slice(const DecodeParams& a, int b, int h0, int len, int p
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
+            // a round past the share in every lane of the wave: nothing to
+            // compute or store (its loads went out with the others')
+            if (__builtin_amdgcn_ballot_w64(st[r] != 0) == 0) continue;
             float bst = neg_inf();
 #pragma unroll
             for (int q = 0; q < COOP_MAX_NREP; ++q) {
@@ -1076,11 +1079,14 @@ void paged_decode_kernel(const DecodeParams a) {
                 const int per = (a.score_pages + Sb - 1) / Sb;
                 const int p_lo = gw.s * per;
                 const int p_hi = p_lo + per < a.score_pages ? p_lo + per : a.score_pages;
-                // (shares of up to 64 pages in one batch of 4 rounds, up to
-                // 128 in one of 8: B8 x 32K at 28 splits, 74-page shares,
-                // had taken two batches of 4)
-                if (p_hi - p_lo <= 4 * NWT * (4 / HG))
+                // (a share in one batch: up to 64 pages in 4 rounds, 80 in 5,
+                // 128 in 8; B8 x 32K at 28 splits, 74-page shares, had taken
+                // two batches of 4)
+                constexpr int PPRW = NWT * (4 / HG);     // pages a round
+                if (p_hi - p_lo <= 4 * PPRW)
                     score_slice<NWT, HG, 4>(a, b, h0, len, p_lo, p_hi);
+                else if (p_hi - p_lo <= 5 * PPRW)
+                    score_slice<NWT, HG, 5>(a, b, h0, len, p_lo, p_hi);
                 else
                     score_slice<NWT, HG, 8>(a, b, h0, len, p_lo, p_hi);
                 LS_STAMP(1);
