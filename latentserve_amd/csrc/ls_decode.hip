@@ -1079,16 +1079,12 @@ void paged_decode_kernel(const DecodeParams a) {
                 const int per = (a.score_pages + Sb - 1) / Sb;
                 const int p_lo = gw.s * per;
                 const int p_hi = p_lo + per < a.score_pages ? p_lo + per : a.score_pages;
-                // (a share in one batch: up to 64 pages in 4 rounds, 80 in 5,
-                // 128 in 8; B8 x 32K at 28 splits, 74-page shares, had taken
-                // two batches of 4)
-                constexpr int PPRW = NWT * (4 / HG);     // pages a round
-                if (p_hi - p_lo <= 4 * PPRW)
-                    score_slice<NWT, HG, 4>(a, b, h0, len, p_lo, p_hi);
-                else if (p_hi - p_lo <= 5 * PPRW)
-                    score_slice<NWT, HG, 5>(a, b, h0, len, p_lo, p_hi);
-                else
-                    score_slice<NWT, HG, 8>(a, b, h0, len, p_lo, p_hi);
+                // (batches of 5 rounds: a share of up to 80 pages in one,
+                // the 74-page shares of 14 and 28 splits included, which
+                // batches of 4 had taken in two; one variant only: with
+                // batches of 4, 5 and 8 compiled in, the larger kernel ran
+                // B8 x 32K 0.3 us slower)
+                score_slice<NWT, HG, 5>(a, b, h0, len, p_lo, p_hi);
                 LS_STAMP(1);
                 // the group's score stores complete, then it counts itself in
                 // the word after row (b, h0) (all ones at rest, so the count
@@ -1121,9 +1117,17 @@ void paged_decode_kernel(const DecodeParams a) {
                     }
                 };
                 const Coop fix{a, b, h0 + hh, len, Sb, done};
-                // (rows of up to COOP_MAX_PAGES pages, eight keys a thread)
-                select_row_lin<8, decltype(emit), 1>(row, a.score_pages, n_list, tid, ssm[hh],
-                                                     ssm[0].vote, emit, fix);
+                // (rows of up to COOP_MAX_PAGES pages: eight keys a thread;
+                // up to 1024, four, half the work a thread: B16 x 16K 40.6 ->
+                // 39.5 us.  In this order: with the four-key branch first,
+                // the eight-key rows ran 0.45 us slower, B8 x 32K 42.7 ->
+                // 43.1 us)
+                if (a.score_pages > 4 * 256)
+                    select_row_lin<8, decltype(emit), 1>(row, a.score_pages, n_list, tid, ssm[hh],
+                                                         ssm[0].vote, emit, fix);
+                else
+                    select_row_lin<4, decltype(emit), 1>(row, a.score_pages, n_list, tid, ssm[hh],
+                                                         ssm[0].vote, emit, fix);
             } else {
                 if (a.score_pages <= 8 * 256)
                     select_row_lin<8>(row, a.score_pages, n_list, tid, ssm[hh], ssm[0].vote, emit);
